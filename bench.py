@@ -1,0 +1,166 @@
+"""Benchmark of the fused LNCC loss hot path on one MI355X.
+
+One step = ``fused_lncc_loss(pred, target, 7).backward()`` with ``pred.grad = None`` first, on the
+headline workload (2,16,128,128,128) fp32, k=7 (target ~ N(0,1) seed 0, pred = 0.8 target +
+0.6 N(0,1) seed 1; CPU-generated, resident in HBM before timing). Prints one JSON line:
+
+* value / unit: algorithmic HBM throughput of the whole step, 12 B per voxel (read pred, read
+  target, write grad once) / ms_per_step, in GB/s;
+* roofline: the fused kernel alone (lncc_fused_kernel), timed with HIP events on the stream it is
+  launched on, against the 8 TB/s HBM peak; traffic = FETCH_SIZE + WRITE_SIZE per launch from the
+  committed rocprofv3 counter summary when present;
+* cpu_baseline: the reference's naive PyTorch LNCC (dense grouped conv3d + autograd, restated in
+  oracle/torch_lncc_port.py) on the host cores, on one of the 32 volumes.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _sub in ("fused-lncc_amd", "oracle", os.path.join("tests", "golden")):
+    sys.path.insert(0, os.path.join(ROOT, _sub))
+
+HBM_PEAK_GBS = 8000.0
+BYTES_PER_VOXEL = {"float32": 12, "bfloat16": 6}
+METRIC = "fwd+bwd ms & achieved HBM GB/s (% of peak), (2,16,128³) fp32 k=7, 1 GPU"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "lncc_fused_kernel_headline_pmc.json")
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=12)
+    ap.add_argument("--workload", default="headline", choices=["headline", "bf16", "mri", "large"])
+    ap.add_argument("--kernel-reps", type=int, default=40)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_baseline(k, seconds):
+    import torch
+
+    import torch_lncc_port
+    import workloads as wl
+    shape = (1, 1, 128, 128, 128)
+    p, t = wl.make_inputs("headline", shape)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while True:
+        t0 = time.perf_counter()
+        torch_lncc_port.loss_and_grad(p, t, k)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() >= t_end or len(times) >= 50:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    vox = 128 ** 3
+    return {"value": round(vox * 12 / med / 1e9, 6), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"1 of the 32 volumes, (1,1,128,128,128) fp32 k=7, loss + grad wrt pred; "
+                      f"median of {len(times)} runs = {med * 1e3:.1f} ms "
+                      f"({vox / med / 1e6:.3f} Mvoxel/s) on {torch.get_num_threads()} threads"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested). The loss is "
+              "independent per (N,C) volume; multi-GPU use is data-parallel with no collective in "
+              "the loss, see DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import workloads as wl
+    from fused_lncc import _lib, fused_lncc_loss
+
+    spec = wl.WORKLOADS[a.workload]
+    k = spec["k"]
+    p, t = wl.make_inputs(a.workload)
+    dev = torch.device("cuda:0")
+    p = p.to(dev).requires_grad_(True)
+    t = t.to(dev)
+    dtname = str(p.dtype).replace("torch.", "")
+    V = p.numel()
+    torch.cuda.synchronize()
+
+    def step():
+        p.grad = None
+        fused_lncc_loss(p, t, k).backward()
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(a.steps + 1)]
+    evs[0].record()
+    for i in range(a.steps):
+        step()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    total_ms = evs[0].elapsed_time(evs[-1])
+    per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(a.steps))
+    ms_per_step = total_ms / a.steps
+    median_ms = per[len(per) // 2]
+
+    # the fused kernel alone, on the stream it is launched on
+    lib = _lib.load()
+    B = spec["shape"][0] * spec["shape"][1]
+    D, H, W = spec["shape"][2:]
+    code = _lib.FL_BF16 if p.dtype == torch.bfloat16 else _lib.FL_F32
+    nbytes = lib.fl_workspace_bytes(B, D, H, W, k)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    grad = torch.empty_like(p)
+    stream = torch.cuda.current_stream(dev)
+    kev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * a.kernel_reps)]
+    for i in range(a.kernel_reps + 3):
+        if i >= 3:
+            kev[2 * (i - 3)].record(stream)
+        _lib.check(lib.fl_lncc_fused_partials(p.data_ptr(), t.data_ptr(), code, B, D, H, W, k, 1e-5,
+                                              grad.data_ptr(), ws.data_ptr(), nbytes, stream.cuda_stream))
+        if i >= 3:
+            kev[2 * (i - 3) + 1].record(stream)
+    torch.cuda.synchronize()
+    kms = [kev[2 * i].elapsed_time(kev[2 * i + 1]) for i in range(a.kernel_reps)]
+    kernel_ms = sum(kms) / len(kms)
+    alg_bytes = V * BYTES_PER_VOXEL[dtname]
+    achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            prof = json.load(f)
+        if prof.get("workload") == a.workload:
+            traffic = prof.get("hbm_bytes_per_launch")
+
+    out = {
+        "metric": METRIC if a.workload == "headline" else f"fwd+bwd GB/s, {a.workload} {spec['shape']} k={k}",
+        "value": round(alg_bytes / (ms_per_step * 1e-3) / 1e9, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "median_ms": round(median_ms, 5),
+        "kernel_ms": round(kernel_ms, 5),
+        "voxels_per_s": round(V / (ms_per_step * 1e-3), 1),
+        "pct_of_hbm_peak": round(100.0 * alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if dtname == "float32" else "bf16 (f32 accumulate)",
+        "data": "synthetic",
+        "config": {"workload": f"lncc fwd+bwd {a.workload}", "shape": list(spec["shape"]), "kernel_size": k,
+                   "input_dtype": dtname, "bytes_per_voxel": BYTES_PER_VOXEL[dtname]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
+                     "kernel": "lncc_fused_kernel", "algorithmic_bytes_per_launch": alg_bytes},
+    }
+    if not a.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(k, a.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

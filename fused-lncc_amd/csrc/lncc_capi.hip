@@ -1,0 +1,255 @@
+// C ABI of libfused_lncc_hip.so (declared in include/fused_lncc.h): host-side validation, launch
+// planning (tiles, D-chunks), and the launches. No allocation and no host synchronization.
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <string>
+
+#include "../../include/fused_lncc.h"
+#include "lncc_common.h"
+#include "lncc_launch.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    g_err = std::string(what) + ": " + hipGetErrorString(e);
+    return FL_E_DEVICE;
+}
+
+constexpr int64_t kMaxPlaneBytes = 0x7fffffffLL;  // per-plane buffer offsets are 31-bit
+
+struct Plan {
+    int ntx, nty, nzc, dchunk;
+    uint32_t nblocks;
+};
+
+// Workgroups: B volumes x (W/TX) x (H/TY) tiles x D-chunks. A chunk of d output planes costs d+4h
+// pipeline steps, so D is split only as far as needed to give the device at least two rounds of
+// workgroups (one workgroup per CU); FUSED_LNCC_DCHUNK overrides the chunk length for tuning.
+Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
+    Plan p;
+    p.ntx = (int)((W + fl::TX - 1) / fl::TX);
+    p.nty = (int)((H + fl::TY - 1) / fl::TY);
+    const int64_t base = B * p.ntx * p.nty;
+    const int64_t target = 512;
+    const int64_t minchunk = 4 * halo > 8 ? 4 * halo : 8;
+    int64_t nzc = (target + base - 1) / base;
+    int64_t maxz = D / minchunk;
+    if (maxz < 1) maxz = 1;
+    if (nzc > maxz) nzc = maxz;
+    if (nzc < 1) nzc = 1;
+    int64_t dchunk = (D + nzc - 1) / nzc;
+    if (const char* e = getenv("FUSED_LNCC_DCHUNK")) {
+        const long v = strtol(e, nullptr, 10);
+        if (v > 0) dchunk = v < D ? v : D;
+    }
+    p.dchunk = (int)dchunk;
+    p.nzc = (int)((D + dchunk - 1) / dchunk);
+    p.nblocks = (uint32_t)(base * p.nzc);
+    return p;
+}
+
+int check_shape(int64_t B, int64_t D, int64_t H, int64_t W, int elem) {
+    if (B < 1 || D < 1 || H < 1 || W < 1) return fail(FL_E_SHAPE, "fused_lncc: empty volume (B, D, H, W must be >= 1)");
+    if (H * W * elem > kMaxPlaneBytes) return fail(FL_E_SHAPE, "fused_lncc: one (H, W) plane exceeds 2 GiB");
+    if (D > (1 << 30)) return fail(FL_E_SHAPE, "fused_lncc: D too large");
+    const int64_t tiles = B * ((W + fl::TX - 1) / fl::TX) * ((H + fl::TY - 1) / fl::TY) * D;
+    if (tiles > 0x7fffffffLL) return fail(FL_E_SHAPE, "fused_lncc: too many volumes/tiles for one launch");
+    return FL_OK;
+}
+
+int check_k(int k) {
+    if (k < 3 || k > 9 || (k % 2) == 0)
+        return fail(FL_E_KSIZE, "fused_lncc: kernel_size must be odd and in 3..9, got " + std::to_string(k));
+    return FL_OK;
+}
+
+int check_dtype(int dtype) {
+    if (dtype != FL_F32 && dtype != FL_BF16)
+        return fail(FL_E_DTYPE, "fused_lncc: float32 or bfloat16 only (dtype code " + std::to_string(dtype) + ")");
+    return FL_OK;
+}
+
+hipError_t launch_fused(int halo, int mode, bool bf16, const fl::FusedArgs& a, uint32_t nb, hipStream_t st) {
+    switch (halo) {
+        case 1: return fl::launch_fused_h1(mode, bf16, a, nb, st);
+        case 2: return fl::launch_fused_h2(mode, bf16, a, nb, st);
+        case 3: return fl::launch_fused_h3(mode, bf16, a, nb, st);
+        case 4: return fl::launch_fused_h4(mode, bf16, a, nb, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int fl_version(void) { return (0 << 16) | (1 << 8) | 0; }
+
+const char* fl_last_error(void) { return g_err.c_str(); }
+
+int fl_validate(int dtype, int kernel_size, int64_t B, int64_t D, int64_t H, int64_t W) {
+    int rc = check_dtype(dtype);
+    if (rc) return rc;
+    rc = check_k(kernel_size);
+    if (rc) return rc;
+    return check_shape(B, D, H, W, dtype == FL_BF16 ? 2 : 4);
+}
+
+size_t fl_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size) {
+    if (check_k(kernel_size) || check_shape(B, D, H, W, 4)) return 0;
+    return (size_t)plan_fused(B, D, H, W, kernel_size / 2).nblocks * sizeof(double);
+}
+
+int fl_lncc_fused_partials(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,
+                           int64_t W, int kernel_size, float smooth_dr, void* grad, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    int rc = fl_validate(dtype, kernel_size, B, D, H, W);
+    if (rc) return rc;
+    if (!pred || !target || !workspace) return fail(FL_E_NULL, "fl_lncc_fused_partials: NULL pointer argument");
+    const int halo = kernel_size / 2;
+    const Plan p = plan_fused(B, D, H, W, halo);
+    if (workspace_bytes < (size_t)p.nblocks * sizeof(double))
+        return fail(FL_E_WORKSPACE, "fl_lncc_fused_partials: workspace needs " +
+                                        std::to_string((size_t)p.nblocks * sizeof(double)) + " bytes");
+    const double M = (double)B * (double)D * (double)H * (double)W;
+    fl::FusedArgs a = {};
+    a.pred = pred;
+    a.target = target;
+    a.grad = grad;
+    a.partials = static_cast<double*>(workspace);
+    a.dimD = (int)D;
+    a.dimH = (int)H;
+    a.dimW = (int)W;
+    a.ntx = p.ntx;
+    a.nty = p.nty;
+    a.nzc = p.nzc;
+    a.dchunk = p.dchunk;
+    a.inv_n = (float)(1.0 / ((double)kernel_size * kernel_size * kernel_size));
+    a.dr = smooth_dr;
+    a.gscale = (float)(2.0 / M);
+    hipError_t e = launch_fused(halo, grad ? fl::MODE_GRAD : fl::MODE_LOSS, dtype == FL_BF16, a, p.nblocks,
+                                static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "fl_lncc_fused_partials: fused kernel launch");
+    return FL_OK;
+}
+
+int fl_lncc_finalize(const void* workspace, int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size,
+                     float* loss, void* stream) {
+    int rc = fl_validate(FL_F32, kernel_size, B, D, H, W);
+    if (rc) return rc;
+    if (!workspace || !loss) return fail(FL_E_NULL, "fl_lncc_finalize: NULL pointer argument");
+    const Plan p = plan_fused(B, D, H, W, kernel_size / 2);
+    const double M = (double)B * (double)D * (double)H * (double)W;
+    hipError_t e = fl::launch_finalize(static_cast<const double*>(workspace), (int)p.nblocks, 1.0 / M, loss,
+                                       static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "fl_lncc_finalize: launch");
+    return FL_OK;
+}
+
+int fl_lncc_loss_grad(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,
+                      int64_t W, int kernel_size, float smooth_dr, float* loss, void* grad, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+    if (!loss) {
+        int rc = fl_validate(dtype, kernel_size, B, D, H, W);
+        return rc ? rc : fail(FL_E_NULL, "fl_lncc_loss_grad: NULL pointer argument");
+    }
+    int rc = fl_lncc_fused_partials(pred, target, dtype, B, D, H, W, kernel_size, smooth_dr, grad, workspace,
+                                    workspace_bytes, stream);
+    if (rc) return rc;
+    return fl_lncc_finalize(workspace, B, D, H, W, kernel_size, loss, stream);
+}
+
+int fl_scale_grad(void* grad, int dtype, int64_t n, const float* grad_out, void* stream) {
+    int rc = check_dtype(dtype);
+    if (rc) return rc;
+    if (n < 0) return fail(FL_E_SHAPE, "fl_scale_grad: negative element count");
+    if (n == 0) return FL_OK;
+    if (!grad || !grad_out) return fail(FL_E_NULL, "fl_scale_grad: NULL pointer argument");
+    hipError_t e = fl::launch_scale(grad, dtype == FL_BF16, n, grad_out, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "fl_scale_grad: launch");
+    return FL_OK;
+}
+
+int fl_lncc_maps(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H, int64_t W,
+                 int kernel_size, float smooth_dr, float* ncc, float* A, float* Bc, float* Cc, void* stream) {
+    int rc = fl_validate(dtype, kernel_size, B, D, H, W);
+    if (rc) return rc;
+    if (!pred || !target || !ncc || !A || !Bc || !Cc) return fail(FL_E_NULL, "fl_lncc_maps: NULL pointer argument");
+    const int halo = kernel_size / 2;
+    const Plan p = plan_fused(B, D, H, W, halo);
+    fl::FusedArgs a = {};
+    a.pred = pred;
+    a.target = target;
+    a.ncc_map = ncc;
+    a.a_map = A;
+    a.b_map = Bc;
+    a.c_map = Cc;
+    a.partials = nullptr;
+    a.dimD = (int)D;
+    a.dimH = (int)H;
+    a.dimW = (int)W;
+    a.ntx = p.ntx;
+    a.nty = p.nty;
+    a.nzc = p.nzc;
+    a.dchunk = p.dchunk;
+    a.inv_n = (float)(1.0 / ((double)kernel_size * kernel_size * kernel_size));
+    a.dr = smooth_dr;
+    a.gscale = 0.f;
+    hipError_t e = launch_fused(halo, fl::MODE_MAPS, dtype == FL_BF16, a, p.nblocks, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "fl_lncc_maps: launch");
+    return FL_OK;
+}
+
+int fl_lncc_backward(const float* A, const float* Bc, const float* Cc, const void* pred, const void* target,
+                     int dtype, int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size, float scale,
+                     void* grad, void* stream) {
+    int rc = fl_validate(dtype, kernel_size, B, D, H, W);
+    if (rc) return rc;
+    if (!A || !Bc || !Cc || !pred || !target || !grad) return fail(FL_E_NULL, "fl_lncc_backward: NULL pointer argument");
+    fl::BoxArgs a = {};
+    a.f0 = A;
+    a.f1 = Bc;
+    a.f2 = Cc;
+    a.pred = pred;
+    a.target = target;
+    a.out = grad;
+    a.dimD = (int)D;
+    a.dimH = (int)H;
+    a.dimW = (int)W;
+    a.ntx = (int)((W + 15) / 16);
+    a.nty = (int)((H + 15) / 16);
+    a.scale = scale;
+    const uint32_t nb = (uint32_t)(B * a.ntx * a.nty);
+    hipError_t e = fl::launch_box(kernel_size / 2, 3, dtype == FL_BF16, a, nb, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "fl_lncc_backward: launch");
+    return FL_OK;
+}
+
+int fl_box3d(const float* x, float* y, int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size, void* stream) {
+    int rc = fl_validate(FL_F32, kernel_size, B, D, H, W);
+    if (rc) return rc;
+    if (!x || !y) return fail(FL_E_NULL, "fl_box3d: NULL pointer argument");
+    fl::BoxArgs a = {};
+    a.f0 = x;
+    a.out = y;
+    a.dimD = (int)D;
+    a.dimH = (int)H;
+    a.dimW = (int)W;
+    a.ntx = (int)((W + 15) / 16);
+    a.nty = (int)((H + 15) / 16);
+    a.scale = 1.f;
+    const uint32_t nb = (uint32_t)(B * a.ntx * a.nty);
+    hipError_t e = fl::launch_box(kernel_size / 2, 1, false, a, nb, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "fl_box3d: launch");
+    return FL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,11 @@
+// Instantiations and launcher of the fused LNCC kernel for k = 3 (halo 1).
+#include "lncc_fused_kernel.h"
+#include "lncc_launch.h"
+
+namespace fl {
+
+hipError_t launch_fused_h1(int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st) {
+    return launch_fused<1>(mode, bf16, a, nblocks, st);
+}
+
+}  // namespace fl

@@ -1,0 +1,46 @@
+// Host-side view of the kernel launchers (argument blocks and per-halo entry points).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fl {
+
+enum Mode { MODE_LOSS = 0, MODE_GRAD = 1, MODE_MAPS = 2 };
+
+struct FusedArgs {
+    const void* pred;
+    const void* target;
+    void* grad;       // MODE_GRAD: gradient wrt pred, pred dtype
+    float* ncc_map;   // MODE_MAPS: fp32 maps ncc, A, Bc, Cc (reference definitions)
+    float* a_map;
+    float* b_map;
+    float* c_map;
+    double* partials; // one ncc partial sum per workgroup
+    int dimD, dimH, dimW;
+    int ntx, nty, nzc, dchunk;
+    float inv_n, dr, gscale;  // gscale = 2/M
+};
+
+struct BoxArgs {
+    const float* f0;  // fields to box-sum (f1, f2 only for the three-field combine)
+    const float* f1;
+    const float* f2;
+    const void* pred;   // combine: p, t in the pred dtype
+    const void* target;
+    void* out;          // box3d: fp32 sum; combine: gradient in the pred dtype
+    int dimD, dimH, dimW;
+    int ntx, nty;
+    float scale;
+};
+
+hipError_t launch_fused_h1(int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
+hipError_t launch_fused_h2(int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
+hipError_t launch_fused_h3(int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
+hipError_t launch_fused_h4(int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
+
+// box3d (nfields = 1, fp32 out) and the reference backward combine (nfields = 3)
+hipError_t launch_box(int halo, int nfields, bool bf16, const BoxArgs& a, uint32_t nblocks, hipStream_t st);
+hipError_t launch_finalize(const double* partials, int nparts, double inv_m, float* loss, hipStream_t st);
+hipError_t launch_scale(void* grad, bool bf16, int64_t n, const float* grad_out, hipStream_t st);
+
+}  // namespace fl

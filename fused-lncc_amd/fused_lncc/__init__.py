@@ -1,0 +1,130 @@
+"""Fused 3D local (squared) normalized cross-correlation loss for AMD MI355X (gfx950).
+
+Drop-in for the reference's ``fused_lncc`` package (fused_lncc/__init__.py:77-83):
+
+    from fused_lncc import fused_lncc_loss
+    loss = fused_lncc_loss(pred, target, kernel_size=7, smooth_dr=1e-5)   # 1 - mean(ncc)
+    loss.backward()                                                        # grad to pred only
+
+``pred``/``target`` are (N, C, D, H, W) float32 or bfloat16 tensors on a ROCm device; the loss is a
+0-d float32 tensor, the gradient has the pred dtype. The forward runs one hand-written HIP kernel
+that reads pred and target once and writes the gradient (already scaled by -1/M) together with
+per-workgroup partial sums of ncc; a one-workgroup kernel turns those into the loss. The backward
+only multiplies by ``grad_out`` on the device, skipping the work when it is 1, so a
+``loss.backward()`` moves 12 bytes per fp32 voxel through HBM and never synchronizes with the host.
+"""
+import torch
+
+from . import _lib, ext
+
+__all__ = ["fused_lncc_loss", "ext"]
+
+
+# Custom ops keep the loss traceable by torch.compile (fused_lncc/__init__.py:22-46). Fake kernels
+# give the loss as float32 whatever the input dtype, and the gradient in the input dtype.
+@torch.library.custom_op("fused_lncc::loss_grad", mutates_args=())
+def _loss_grad_op(pf: torch.Tensor, tf: torch.Tensor, kernel_size: int, smooth_dr: float,
+                  need_grad: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    loss, grad = ext.loss_grad(pf, tf, kernel_size, smooth_dr, need_grad)
+    if grad is None:
+        grad = pf.new_empty((0,))
+    return loss, grad
+
+
+@_loss_grad_op.register_fake
+def _(pf, tf, kernel_size, smooth_dr, need_grad):
+    loss = pf.new_empty((), dtype=torch.float32)
+    return loss, (torch.empty_like(pf) if need_grad else pf.new_empty((0,)))
+
+
+@torch.library.custom_op("fused_lncc::scale_grad_", mutates_args=("grad",))
+def _scale_grad_op(grad: torch.Tensor, grad_out: torch.Tensor) -> None:
+    ext.scale_grad_(grad, grad_out)
+
+
+@_scale_grad_op.register_fake
+def _(grad, grad_out):
+    return None
+
+
+# The reference's two building-block ops, same names and signatures (fused_lncc/__init__.py:26-46).
+@torch.library.custom_op("fused_lncc::forward", mutates_args=())
+def _lncc_forward_op(pf: torch.Tensor, tf: torch.Tensor, kernel_size: int, smooth_dr: float) -> list[torch.Tensor]:
+    return ext.lncc_forward(pf, tf, kernel_size, smooth_dr)
+
+
+@_lncc_forward_op.register_fake
+def _(pf, tf, kernel_size, smooth_dr):
+    return [torch.empty_like(pf, dtype=torch.float32) for _ in range(4)]
+
+
+@torch.library.custom_op("fused_lncc::backward", mutates_args=())
+def _lncc_backward_op(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, pf: torch.Tensor,
+                      tf: torch.Tensor, kernel_size: int, scale: float) -> torch.Tensor:
+    return ext.lncc_backward(A, B, C, pf, tf, kernel_size, scale)
+
+
+@_lncc_backward_op.register_fake
+def _(A, B, C, pf, tf, kernel_size, scale):
+    return torch.empty_like(pf)
+
+
+def _compiling():
+    try:
+        return torch.compiler.is_compiling()
+    except AttributeError:  # pragma: no cover
+        return False
+
+
+class _FusedLNCC(torch.autograd.Function):
+    """Autograd wrapper: the gradient is produced in forward by the fused kernel and handed out in
+    backward (fused_lncc/__init__.py:49-74 computes it in backward from four saved fp32 maps)."""
+
+    @staticmethod
+    def forward(ctx, pred, target, kernel_size, smooth_dr, need_grad):
+        N, C = pred.shape[:2]
+        S = pred.shape[2:]
+        pf = pred.reshape(N * C, *S)
+        tf = target.reshape(N * C, *S)
+        need = bool(need_grad and ctx.needs_input_grad[0])
+        loss, grad = torch.ops.fused_lncc.loss_grad(pf, tf, kernel_size, smooth_dr, need)
+        ctx.k = kernel_size
+        ctx.dr = smooth_dr
+        ctx.shape = pred.shape
+        ctx.grad = None
+        if need:
+            if _compiling():
+                ctx.save_for_backward(pf, tf, grad)
+            else:
+                # kept outside save_for_backward so the first backward can scale it in place and
+                # hand it to AccumulateGrad without a copy
+                ctx.grad = grad
+                ctx.save_for_backward(pf, tf)
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        saved = ctx.saved_tensors
+        pf, tf = saved[0], saved[1]
+        if len(saved) == 3:  # traced: functional form
+            g = saved[2] * grad_out.to(saved[2].dtype)
+            return g.reshape(ctx.shape), None, None, None, None
+        g = ctx.grad
+        ctx.grad = None
+        if g is None:  # second backward through a retained graph: recompute
+            _, g = torch.ops.fused_lncc.loss_grad(pf, tf, ctx.k, ctx.dr, True)
+        torch.ops.fused_lncc.scale_grad_(g, grad_out.detach())
+        return g.reshape(ctx.shape), None, None, None, None
+
+
+def fused_lncc_loss(pred, target, kernel_size=7, smooth_dr=1e-5):
+    """1 - mean(squared local NCC) over all voxels. Gradient flows through ``pred`` only.
+
+    pred, target: (N, C, D, H, W) float32 or bfloat16 ROCm tensors; kernel_size odd in 3..9.
+    Returns a 0-d float32 loss in [0, 1] (fused_lncc/__init__.py:77-83)."""
+    assert pred.dim() == 5 and pred.shape == target.shape, "expect matching (N,C,D,H,W)"
+    assert kernel_size % 2 == 1, "kernel_size must be odd"
+    # The gradient is computed in the forward kernel only when autograd will ask for it; under
+    # no_grad or for a pred without requires_grad the kernel reads 8 B/voxel and writes nothing.
+    need_grad = torch.is_grad_enabled() and pred.requires_grad
+    return _FusedLNCC.apply(pred.contiguous(), target.contiguous(), kernel_size, smooth_dr, need_grad)

@@ -1,0 +1,89 @@
+"""Synthetic input recipes for the LNCC workloads (CPU-generated, bit-identical across machines).
+
+Every tensor is drawn on the CPU from a seeded ``torch.Generator`` and only then moved to a
+device, so the GPU tests, the fixtures and the benchmark all see the same bytes.
+
+Workloads (pred, target are (N, C, D, H, W)):
+
+* ``cpu``      (1,1,32,32,32) fp32, k=3: target ~ U[0,1) seed 0, pred = 0.7*target + 0.3*U[0,1) seed 1.
+* ``mri``      (1,1,160,192,224) fp32, k=9: target = N(0,1) seed 0, Gaussian-smoothed (sigma 2 voxels,
+  separable, truncated at 4 sigma, reflect padding, float64), min-max scaled to [0,1];
+  pred = roll(target, +2 along W) + 0.05*N(0,1) seed 1.
+* ``headline`` (2,16,128,128,128) fp32, k=7: target ~ N(0,1) seed 0, pred = 0.8*target + 0.6*N(0,1) seed 1.
+* ``bf16``     the headline recipe at (2,16,128,128,128) built in fp32, cast to bf16, k=5.
+* ``large``    the headline recipe at (2,16,256,256,256) fp32, k=7.
+"""
+import math
+
+import numpy as np
+import torch
+
+WORKLOADS = {
+    "cpu": dict(shape=(1, 1, 32, 32, 32), k=3, dtype="float32"),
+    "mri": dict(shape=(1, 1, 160, 192, 224), k=9, dtype="float32"),
+    "headline": dict(shape=(2, 16, 128, 128, 128), k=7, dtype="float32"),
+    "bf16": dict(shape=(2, 16, 128, 128, 128), k=5, dtype="bfloat16"),
+    "large": dict(shape=(2, 16, 256, 256, 256), k=7, dtype="float32"),
+}
+
+
+def _gen(seed):
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    return g
+
+
+def _gauss_smooth_f64(x, sigma=2.0):
+    """Separable Gaussian (truncated at 4 sigma, reflect padding) over the last three axes, float64."""
+    r = int(math.ceil(4 * sigma))
+    taps = np.exp(-0.5 * (np.arange(-r, r + 1) / sigma) ** 2)
+    taps /= taps.sum()
+    y = x.astype(np.float64)
+    for ax in (-3, -2, -1):
+        pad = [(0, 0)] * y.ndim
+        pad[ax] = (r, r)
+        yp = np.pad(y, pad, mode="reflect")
+        n = y.shape[ax]
+        acc = np.zeros_like(y)
+        for i, w in enumerate(taps):
+            acc += w * np.take(yp, np.arange(i, i + n), axis=ax)
+        y = acc
+    return y
+
+
+def make_inputs(name, shape=None):
+    """Return (pred, target) as CPU tensors for workload ``name`` (optionally at another shape)."""
+    spec = WORKLOADS[name]
+    shape = tuple(shape or spec["shape"])
+    if name == "cpu":
+        t = torch.rand(shape, generator=_gen(0))
+        p = 0.7 * t + 0.3 * torch.rand(shape, generator=_gen(1))
+    elif name == "mri":
+        noise = torch.randn(shape, generator=_gen(0)).numpy()
+        sm = _gauss_smooth_f64(noise)
+        sm = (sm - sm.min()) / (sm.max() - sm.min())
+        t = torch.from_numpy(sm.astype(np.float32))
+        p = torch.roll(t, shifts=2, dims=-1) + 0.05 * torch.randn(shape, generator=_gen(1))
+    elif name in ("headline", "bf16", "large"):
+        t = torch.randn(shape, generator=_gen(0))
+        p = 0.8 * t + 0.6 * torch.randn(shape, generator=_gen(1))
+        if name == "bf16":
+            t, p = t.to(torch.bfloat16), p.to(torch.bfloat16)
+    else:
+        raise KeyError(name)
+    return p.contiguous(), t.contiguous()
+
+
+def randn_pair(shape, seed, dtype=torch.float32):
+    """Independent N(0,1) pred/target pair, the input style of the reference's own tests."""
+    g = _gen(seed)
+    p = torch.randn(shape, generator=g)
+    t = torch.randn(shape, generator=g)
+    return p.to(dtype).contiguous(), t.to(dtype).contiguous()
+
+
+def checksum(x):
+    """Order-fixed float64 digest of a tensor: (sum, sum of squares, weighted sum)."""
+    a = x.detach().to(torch.float64).reshape(-1).cpu().numpy()
+    w = np.cos(np.arange(a.size, dtype=np.float64) * 0.001)
+    return [float(np.sum(a)), float(np.sum(a * a)), float(np.dot(a, w))]

@@ -1,0 +1,312 @@
+"""GPU parity of the HIP path against the reference's golden vectors and the CPU oracle.
+
+Mirrors the reference's own tests (tests/test_pytest.py, test_fixes.py, test_robust.py,
+test_bf16.py, verify_fwd.py, verify_bwd.py) with the north-star bar:
+  fp32 loss relative error <= 1e-5, bf16 loss relative error <= 1e-2,
+  gradient cosine > 0.9999 and relative L2 error < 1e-3.
+Inputs are generated on the CPU (seeded), so every run sees the same bytes.
+"""
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle as O
+import workloads as wl
+from fused_lncc import ext, fused_lncc_loss
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+FULL = sorted(f for f in glob.glob(os.path.join(GOLDEN, "*.npz")) if not os.path.basename(f).startswith("stats_"))
+PARITY = [f for f in FULL if not os.path.basename(f).startswith("degen_")]
+
+LOSS_RTOL_F32 = 1e-5
+LOSS_RTOL_BF16 = 1e-2
+GRAD_COS = 0.9999
+GRAD_REL_L2 = 1e-3
+
+
+def fused(p, t, k, dr=1e-5, dtype=None):
+    """fused_lncc_loss + backward on the GPU; returns (loss, grad as float64 numpy, grad dtype)."""
+    p = torch.as_tensor(p)
+    t = torch.as_tensor(t)
+    if dtype is not None:
+        p, t = p.to(dtype), t.to(dtype)
+    pd = p.to(DEV).requires_grad_(True)
+    loss = fused_lncc_loss(pd, t.to(DEV), k, dr)
+    loss.backward()
+    torch.cuda.synchronize()
+    return float(loss.item()), pd.grad.double().cpu().numpy(), pd.grad.dtype
+
+
+def cos_rel(g, gr):
+    g = np.asarray(g, np.float64).ravel()
+    gr = np.asarray(gr, np.float64).ravel()
+    n = np.linalg.norm(gr)
+    return float(g @ gr / (np.linalg.norm(g) * n)), float(np.linalg.norm(g - gr) / n)
+
+
+def assert_grad(g, gr, cos_min=GRAD_COS, rel_max=GRAD_REL_L2):
+    c, r = cos_rel(g, gr)
+    assert c > cos_min and r < rel_max, f"cos={c:.8f} relL2={r:.3e}"
+
+
+def assert_loss(l, lr, rtol):
+    assert abs(l - lr) <= rtol * abs(lr), f"loss {l:.9f} vs {lr:.9f} (rel {abs(l - lr) / abs(lr):.2e})"
+
+
+# ---------------------------------------------------------------- golden vectors (reference outputs)
+@pytest.mark.parametrize("path", PARITY, ids=[os.path.basename(p)[:-4] for p in PARITY])
+def test_golden_vectors(path):
+    d = np.load(path)
+    loss, g, _ = fused(d["pred"], d["target"], int(d["k"]), float(d["smooth_dr"]))
+    assert_loss(loss, float(d["loss"]), LOSS_RTOL_F32)
+    assert_grad(g, d["grad"])
+
+
+def test_golden_bf16_values():
+    d = np.load(os.path.join(GOLDEN, "bf16vals_k7.npz"))
+    loss, g, gdt = fused(d["pred"], d["target"], 7, dtype=torch.bfloat16)
+    assert gdt == torch.bfloat16
+    assert_loss(loss, float(d["loss"]), LOSS_RTOL_BF16)
+    assert_grad(g, d["grad"], 0.999, 1e-2)
+
+
+# ---------------------------------------------------------------- reference tests, restated
+@pytest.mark.parametrize("k", [3, 5, 7, 9])
+def test_forward_matches_reference(k):
+    p, t = wl.randn_pair((2, 4, 32, 32, 32), 0)
+    loss, _, _ = fused(p, t, k)
+    lr, _ = O.lncc(p.numpy(), t.numpy(), k, grad=False)
+    assert abs(loss - lr) < 1e-4
+    assert_loss(loss, lr, LOSS_RTOL_F32)
+
+
+@pytest.mark.parametrize("shape", [(2, 4, 32, 32, 32), (1, 8, 24, 40, 32)])
+@pytest.mark.parametrize("k", [3, 5, 7, 9])
+def test_backward_matches_reference(k, shape):
+    p, t = wl.randn_pair(shape, 1)
+    loss, g, _ = fused(p, t, k)
+    lr, gr = O.lncc(p.numpy(), t.numpy(), k)
+    assert_loss(loss, lr, LOSS_RTOL_F32)
+    assert_grad(g, gr)
+    assert np.abs(g - gr).mean() / np.abs(gr).mean() < 1e-3
+
+
+def test_bf16_runs():
+    p, t = wl.randn_pair((1, 2, 16, 16, 16), 2, dtype=torch.bfloat16)
+    _, g, gdt = fused(p, t, 7)
+    assert gdt == torch.bfloat16 and np.isfinite(g).all()
+
+
+@pytest.mark.parametrize("k", [3, 7])
+def test_bf16_matches_fp32_of_same_values(k):
+    p, t = wl.randn_pair((2, 4, 40, 40, 40), 3, dtype=torch.bfloat16)
+    lb, gb, _ = fused(p, t, k)
+    lf, gf, _ = fused(p.float(), t.float(), k)
+    assert abs(lb - lf) < 1e-3
+    assert_loss(lb, lf, LOSS_RTOL_BF16)
+    assert np.abs(gb - gf).mean() / np.abs(gf).mean() < 2e-2
+
+
+@pytest.mark.parametrize("k", [3, 5, 7, 9])
+def test_fused_backward_matches_scatter(k):
+    """Reference-API path: maps -> box-sum scatter formula == lncc_backward (tests/test_pytest.py:38-51),
+    and the fused hot-path gradient equals that unfused path."""
+    p, t = wl.randn_pair((2, 3, 24, 20, 28), 4)
+    pf = p.reshape(6, 24, 20, 28).contiguous().to(DEV)
+    tf = t.reshape(6, 24, 20, 28).contiguous().to(DEV)
+    ncc, A, Bc, Cc = ext.lncc_forward(pf, tf, k, 1e-5)
+    sc = -1.0 / ncc.numel()
+    box = lambda x: ext.box3d_sep_forward(x.contiguous(), k)  # noqa: E731
+    ref = sc * (box(A) + 2.0 * pf * box(Bc) + tf * box(Cc))
+    got = ext.lncc_backward(A, Bc, Cc, pf, tf, k, sc)
+    assert (ref - got).abs().max().item() < 1e-8
+    _, g, _ = fused(p, t, k)
+    assert_grad(g.reshape(6, 24, 20, 28), got.double().cpu().numpy(), 0.99999, 1e-4)
+    assert abs((1.0 - ncc.double().mean().item()) - fused(p, t, k)[0]) < 1e-6
+
+
+@pytest.mark.parametrize("shape", [(2, 4, 24, 24, 24), (1, 8, 32, 40, 48)])
+@pytest.mark.parametrize("k", [3, 5, 7])
+def test_maps_match_oracle(k, shape):
+    """Per-voxel ncc map (tests/verify_fwd.py:27-34) and the adjoint maps A, Bc, Cc."""
+    p, t = wl.randn_pair(shape, 5)
+    B = shape[0] * shape[1]
+    pf = p.reshape(B, *shape[2:]).contiguous().to(DEV)
+    tf = t.reshape(B, *shape[2:]).contiguous().to(DEV)
+    maps = [m.double().cpu().numpy().reshape(shape) for m in ext.lncc_forward(pf, tf, k, 1e-5)]
+    _, _, om = O.lncc(p.numpy(), t.numpy(), k, grad=False, maps=True)
+    assert np.abs(maps[0] - om["ncc"]).max() < 1e-3
+    assert maps[0].min() >= 0 and maps[0].max() <= 1
+    for got, key in zip(maps[1:], ("A", "B", "C")):
+        assert np.linalg.norm(got - om[key]) / np.linalg.norm(om[key]) < 1e-3, key
+
+
+@pytest.mark.parametrize("k", [3, 5, 7, 9])
+def test_box3d_matches_oracle(k):
+    x = torch.randn(3, 13, 17, 11, generator=torch.Generator().manual_seed(k))
+    y = ext.box3d_sep_forward(x.to(DEV), k).double().cpu().numpy()
+    yr = O.box3d(x.numpy(), k)
+    assert np.abs(y - yr).max() < 1e-4 * np.abs(yr).max()
+
+
+def test_degenerate_in_range():
+    z = torch.zeros(1, 1, 16, 16, 16)
+    loss, g, _ = fused(z, z, 7)
+    assert loss == 1.0 and np.all(g == 0)
+
+
+@pytest.mark.parametrize("name", ["all-zero", "constant=5", "constant hi=1e4", "near-const"])
+def test_degenerate_battery(name):
+    gen = torch.Generator().manual_seed(6)
+    if name == "all-zero":
+        p = t = torch.zeros(2, 2, 32, 32, 32)
+    elif name == "constant=5":
+        p = t = torch.full((2, 2, 32, 32, 32), 5.0)
+    elif name == "constant hi=1e4":
+        p = t = torch.full((1, 1, 32, 32, 32), 1e4)
+    else:
+        p = torch.full((1, 2, 24, 24, 24), 3.0) + 1e-3 * torch.randn(1, 2, 24, 24, 24, generator=gen)
+        t = torch.full((1, 2, 24, 24, 24), 3.0)
+    loss, g, _ = fused(p, t, 7)
+    assert np.isfinite(loss) and 0.0 <= loss <= 1.0001 and np.isfinite(g).all()
+
+
+@pytest.mark.parametrize("bad", [float("nan"), float("inf")])
+def test_nonfinite_input_gives_nonfinite_loss(bad):
+    p, t = wl.randn_pair((1, 1, 16, 16, 16), 7)
+    p[0, 0, 8, 8, 8] = bad
+    loss = fused_lncc_loss(p.to(DEV), t.to(DEV), 7)
+    assert not torch.isfinite(loss).item()
+
+
+def test_many_volumes():
+    """N*C = 2080 volumes of (128, 8, 8) (tests/test_fixes.py:9-17)."""
+    p, t = wl.randn_pair((2080, 1, 128, 8, 8), 8)
+    loss, g, _ = fused(p, t, 7)
+    lr, gr = O.lncc(p.numpy(), t.numpy(), 7)
+    assert_loss(loss, lr, LOSS_RTOL_F32)
+    assert_grad(g, gr)
+
+
+def test_unsupported_dtype_raises():
+    p = torch.randn(1, 1, 16, 16, 16, device=DEV, dtype=torch.float64)
+    with pytest.raises(RuntimeError):
+        fused_lncc_loss(p, p, 7)
+
+
+# ---------------------------------------------------------------- autograd contract
+def test_grad_out_scaling_and_retain_graph():
+    p, t = wl.randn_pair((1, 2, 20, 24, 28), 9)
+    _, g1, _ = fused(p, t, 5)
+    pd = p.to(DEV).requires_grad_(True)
+    (3.0 * fused_lncc_loss(pd, t.to(DEV), 5)).backward()
+    assert np.array_equal(pd.grad.double().cpu().numpy(), (torch.from_numpy(g1).float() * 3.0).double().numpy())
+    pd.grad = None
+    (0.0 * fused_lncc_loss(pd, t.to(DEV), 5)).backward()
+    assert torch.count_nonzero(pd.grad).item() == 0
+    pd.grad = None
+    loss = fused_lncc_loss(pd, t.to(DEV), 5)
+    loss.backward(retain_graph=True)
+    loss.backward()
+    assert np.array_equal(pd.grad.double().cpu().numpy(), 2.0 * g1)
+
+
+def test_no_grad_and_target_grad():
+    p, t = wl.randn_pair((2, 2, 16, 24, 20), 10)
+    l1, _, _ = fused(p, t, 7)
+    with torch.no_grad():
+        l0 = fused_lncc_loss(p.to(DEV).requires_grad_(True), t.to(DEV), 7).item()
+    assert l0 == l1
+    td = t.to(DEV).requires_grad_(True)
+    pd = p.to(DEV).requires_grad_(True)
+    fused_lncc_loss(pd, td, 7).backward()
+    assert td.grad is None and pd.grad is not None
+
+
+def test_side_stream_and_determinism():
+    p, t = wl.randn_pair((2, 3, 40, 36, 44), 11)
+    l1, g1, _ = fused(p, t, 7)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        pd = p.to(DEV).requires_grad_(True)
+        loss = fused_lncc_loss(pd, t.to(DEV), 7)
+        loss.backward()
+    s.synchronize()
+    assert loss.item() == l1 and np.array_equal(pd.grad.double().cpu().numpy(), g1)
+
+
+# ---------------------------------------------------------------- the five workloads
+def test_workload_cpu():
+    d = np.load(os.path.join(GOLDEN, "cpu_k3.npz"))
+    p, t = wl.make_inputs("cpu")
+    assert np.array_equal(p.numpy(), d["pred"]) and np.array_equal(t.numpy(), d["target"])
+    loss, g, _ = fused(p, t, 3)
+    assert_loss(loss, float(d["loss"]), LOSS_RTOL_F32)
+    assert_grad(g, d["grad"])
+
+
+@pytest.mark.parametrize("name", ["mri", "headline"])
+def test_workload_fp32(name):
+    st = np.load(os.path.join(GOLDEN, f"stats_{name}.npz"))
+    p, t = wl.make_inputs(name)
+    k = int(st["k"])
+    loss, g, _ = fused(p, t, k)
+    assert_loss(loss, float(st["loss"]), LOSS_RTOL_F32)
+    assert abs(np.linalg.norm(g) - float(st["grad_l2"])) < 1e-3 * float(st["grad_l2"])
+    lr, gr = O.lncc(p.numpy(), t.numpy(), k)
+    assert_loss(loss, lr, LOSS_RTOL_F32)
+    assert_grad(g, gr)
+
+
+def test_workload_bf16():
+    st = np.load(os.path.join(GOLDEN, "stats_bf16.npz"))
+    p, t = wl.make_inputs("bf16")
+    loss, g, gdt = fused(p, t, 5)
+    assert gdt == torch.bfloat16
+    assert_loss(loss, float(st["loss"]), LOSS_RTOL_BF16)
+    lr, gr = O.lncc(p.float().numpy(), t.float().numpy(), 5)
+    assert_grad(g, gr, 0.999, 1e-2)
+
+
+def test_workload_large_properties():
+    """(2,16,256^3) fp32 k=7: fits with no intermediate volume; size-independent properties:
+    the loss is the mean of per-volume-group losses and each group's gradient is the full
+    gradient rescaled by the group's share of voxels; repeated runs are bitwise identical."""
+    p, t = wl.make_inputs("large")
+    pd = p.to(DEV)
+    td = t.to(DEV)
+    del p, t
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    pd.requires_grad_(True)
+    loss = fused_lncc_loss(pd, td, 7)
+    loss.backward()
+    torch.cuda.synchronize()
+    extra = torch.cuda.max_memory_allocated() - base
+    vol_bytes = pd.numel() * 4
+    assert extra <= vol_bytes + (64 << 20), f"extra HBM {extra / 1e9:.2f} GB"
+    L = loss.item()
+    assert np.isfinite(L) and 0.0 <= L <= 1.0
+    g = pd.grad.detach().clone()
+    pd.grad = None
+    fused_lncc_loss(pd, td, 7).backward()
+    assert torch.equal(g, pd.grad)
+    pd.grad = None
+    parts = []
+    for lo in range(0, 2, 1):
+        ps = pd.detach()[lo:lo + 1].clone().requires_grad_(True)
+        ls = fused_lncc_loss(ps, td[lo:lo + 1], 7)
+        ls.backward()
+        parts.append(ls.item())
+        gs = ps.grad * 0.5
+        rel = ((gs - g[lo:lo + 1]).norm() / g[lo:lo + 1].norm()).item()
+        assert rel < 1e-6
+        del ps, gs
+    assert abs(np.mean(parts) - L) <= 1e-6 * L

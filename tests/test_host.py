@@ -1,0 +1,118 @@
+"""CPU-side checks of the C ABI and the Python boundary: no kernel is launched here.
+
+* the built library loads and exports every symbol include/fused_lncc.h declares;
+* fl_validate rejects what the reference rejects (fused_lncc/csrc/lncc3d.cu:123,128-129,158,
+  255-260,281; fused_lncc/__init__.py:81-82) before any device work;
+* the Python API raises the reference's exception types;
+* the fake (meta) kernels give torch.compile the right dtypes;
+* the product package never imports the oracle.
+"""
+import ast
+import os
+import re
+
+import pytest
+import torch
+
+import fused_lncc
+from fused_lncc import _lib, ext, fused_lncc_loss
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fused_lncc.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(fl_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.fl_version() >= (0 << 16) | (1 << 8)
+
+
+@pytest.mark.parametrize("dtype,k,shape,code", [
+    (0, 7, (2, 8, 8, 8), _lib.FL_OK),
+    (1, 3, (1, 1, 1, 1), _lib.FL_OK),
+    (2, 7, (2, 8, 8, 8), _lib.FL_E_DTYPE),      # float64 / anything else
+    (0, 11, (2, 8, 8, 8), _lib.FL_E_KSIZE),
+    (0, 6, (2, 8, 8, 8), _lib.FL_E_KSIZE),
+    (0, 1, (2, 8, 8, 8), _lib.FL_E_KSIZE),
+    (0, 7, (0, 8, 8, 8), _lib.FL_E_SHAPE),
+    (0, 7, (1, 8, 0, 8), _lib.FL_E_SHAPE),
+    (0, 7, (1, 2, 1 << 16, 1 << 14), _lib.FL_E_SHAPE),   # one plane > 2 GiB
+])
+def test_validate(dtype, k, shape, code):
+    lib = _lib.load()
+    assert lib.fl_validate(dtype, k, *shape) == code
+    if code != _lib.FL_OK:
+        assert lib.fl_last_error().decode()
+
+
+def test_errors_before_device_work():
+    lib = _lib.load()
+    # NULL pointers are refused on the host, with a message, and nothing is launched
+    rc = lib.fl_lncc_loss_grad(None, None, 0, 1, 8, 8, 8, 7, 1e-5, None, None, None, 0, None)
+    assert rc == _lib.FL_E_NULL and "NULL" in lib.fl_last_error().decode()
+    rc = lib.fl_box3d(None, None, 1, 8, 8, 8, 4, None)
+    assert rc == _lib.FL_E_KSIZE
+    rc = lib.fl_scale_grad(None, 5, 10, None, None)
+    assert rc == _lib.FL_E_DTYPE
+    # a workspace that is too small is refused
+    rc = lib.fl_lncc_loss_grad(8, 8, 0, 1, 8, 8, 8, 7, 1e-5, 8, None, 8, 0, None)
+    assert rc == _lib.FL_E_WORKSPACE
+
+
+def test_workspace_bytes():
+    lib = _lib.load()
+    n = lib.fl_workspace_bytes(32, 128, 128, 128, 7)
+    assert n > 0 and n % 8 == 0
+    assert lib.fl_workspace_bytes(32, 128, 128, 128, 8) == 0
+    assert ext.workspace_bytes((1, 1, 1, 1), 3) == 8
+
+
+def test_python_api_errors():
+    p = torch.randn(1, 1, 8, 8, 8)
+    with pytest.raises(AssertionError):
+        fused_lncc_loss(p, p, 6)                      # even k
+    with pytest.raises(AssertionError):
+        fused_lncc_loss(p, p[:, :, :4], 7)            # shape mismatch
+    with pytest.raises(AssertionError):
+        fused_lncc_loss(p[0], p[0], 7)                # not 5-D
+    with pytest.raises(RuntimeError, match="float32 or bfloat16"):
+        fused_lncc_loss(p.double(), p.double(), 7)    # float64
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        fused_lncc_loss(p, p, 7)                      # CPU tensors: refused, no CPU fallback
+    with pytest.raises(RuntimeError, match="kernel_size"):
+        _lib.check(_lib.load().fl_validate(0, 11, 1, 8, 8, 8))
+
+
+def test_fake_kernels_dtypes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        for dt in (torch.float32, torch.bfloat16):
+            pf = torch.empty(6, 24, 20, 28, dtype=dt, device="cuda" if torch.cuda.is_available() else "cpu")
+            loss, grad = torch.ops.fused_lncc.loss_grad(pf, pf, 7, 1e-5, True)
+            assert loss.dtype == torch.float32 and loss.shape == ()
+            assert grad.dtype == dt and grad.shape == pf.shape
+            outs = torch.ops.fused_lncc.forward(pf, pf, 7, 1e-5)
+            assert len(outs) == 4 and all(o.dtype == torch.float32 for o in outs)
+            g = torch.ops.fused_lncc.backward(outs[1], outs[2], outs[3], pf, pf, 7, 1.0)
+            assert g.dtype == dt
+
+
+def test_product_never_imports_the_oracle():
+    pkg = os.path.dirname(fused_lncc.__file__)
+    for fn in os.listdir(pkg):
+        if fn.endswith(".py"):
+            tree = ast.parse(open(os.path.join(pkg, fn)).read())
+            for node in ast.walk(tree):
+                if isinstance(node, (ast.Import, ast.ImportFrom)):
+                    names = [a.name for a in node.names] + [getattr(node, "module", None) or ""]
+                    assert not any("oracle" in n for n in names), fn
