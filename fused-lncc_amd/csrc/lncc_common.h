@@ -28,7 +28,8 @@ __device__ __forceinline__ float load_elem(__amdgpu_buffer_rsrc_t r, uint32_t vo
         uint32_t u = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, 0, 0);
         return __uint_as_float(u << 16);
     } else {
-        return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0);
+        // the builtin returns the raw 32 bits; reinterpret, do not convert
+        return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0));
     }
 }
 
