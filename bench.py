@@ -37,7 +37,20 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 268 MB device-to-device copy (calibrates HBM byte counters)")
     return ap.parse_args()
+
+
+def copy_probe():
+    """A plain copy kernel of known size: 2^26 float32 read + 2^26 float32 written per launch."""
+    import torch
+    x = torch.randn(1 << 26, device="cuda:0")
+    y = torch.empty_like(x)
+    for _ in range(5):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": x.numel() * 4, "copy_probe_bytes_written": y.numel() * 4}))
 
 
 def cpu_baseline(k, seconds):
@@ -67,6 +80,9 @@ def cpu_baseline(k, seconds):
 
 def main():
     a = parse()
+    if a.copy_probe:
+        copy_probe()
+        return
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested). The loss is "
               "independent per (N,C) volume; multi-GPU use is data-parallel with no collective in "

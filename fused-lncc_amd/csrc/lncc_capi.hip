@@ -35,8 +35,9 @@ struct Plan {
 // workgroups (one workgroup per CU); FUSED_LNCC_DCHUNK overrides the chunk length for tuning.
 Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     Plan p;
+    const int ty = fl::tile_ty(halo);
     p.ntx = (int)((W + fl::TX - 1) / fl::TX);
-    p.nty = (int)((H + fl::TY - 1) / fl::TY);
+    p.nty = (int)((H + ty - 1) / ty);
     const int64_t base = B * p.ntx * p.nty;
     const int64_t target = 512;
     const int64_t minchunk = 4 * halo > 8 ? 4 * halo : 8;
@@ -60,7 +61,7 @@ int check_shape(int64_t B, int64_t D, int64_t H, int64_t W, int elem) {
     if (B < 1 || D < 1 || H < 1 || W < 1) return fail(FL_E_SHAPE, "fused_lncc: empty volume (B, D, H, W must be >= 1)");
     if (H * W * elem > kMaxPlaneBytes) return fail(FL_E_SHAPE, "fused_lncc: one (H, W) plane exceeds 2 GiB");
     if (D > (1 << 30)) return fail(FL_E_SHAPE, "fused_lncc: D too large");
-    const int64_t tiles = B * ((W + fl::TX - 1) / fl::TX) * ((H + fl::TY - 1) / fl::TY) * D;
+    const int64_t tiles = B * ((W + fl::TX - 1) / fl::TX) * ((H + 23) / 24) * D;
     if (tiles > 0x7fffffffLL) return fail(FL_E_SHAPE, "fused_lncc: too many volumes/tiles for one launch");
     return FL_OK;
 }

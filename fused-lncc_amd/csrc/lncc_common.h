@@ -8,10 +8,10 @@
 
 namespace fl {
 
-// Workgroup: 512 lanes (8 wave64s). Output tile: TX x TY columns of one volume, marched along D.
-constexpr int NT = 512;
-constexpr int TX = 64;
-constexpr int TY = 16;
+// Workgroup: 1024 lanes (16 wave64s). Output tile: TX x TY columns of one volume, marched along D.
+constexpr int NT = 1024;
+constexpr int TX = 32;
+constexpr __host__ __device__ inline int tile_ty(int halo) { return halo == 4 ? 24 : 32; }
 
 // gfx9 buffer resource word 3 (raw buffer, 32-bit data format); out-of-range loads return 0 and
 // out-of-range stores are dropped, which gives the zero padding of the box window for free.
@@ -73,42 +73,50 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 constexpr int odd(int a) { return a | 1; }
 
+// Row stride (floats) for LDS rows read as float2 by lanes that step from row to row: even, and
+// = 2 mod 4 so that the 16 lanes served per cycle by a 64-bit read land on distinct bank pairs.
+constexpr int stride2(int n) { return (n % 4 == 2) ? n : (n % 4 == 3 ? n + 3 : (n % 4 == 0 ? n + 2 : n + 1)); }
+constexpr int rup64(int n) { return (n + 63) / 64 * 64; }
+
 // Tile geometry for halo H (k = 2H+1). Coordinates inside a workgroup:
 //   input region   ix in [0,IX), iy in [0,IY)  <-> global (x0-2H+ix, y0-2H+iy)
 //   adjoint region ax in [0,AX), ay in [0,AY)  <-> global (x0-H+ax,  y0-H+ay)
 //   output tile    ox in [0,TX), oy in [0,TY)  <-> global (x0+ox,    y0+oy)
+// Running-sum passes work on segments of S consecutive outputs; a segment that would overrun the
+// range is shifted back to end at the range's end (its first outputs then repeat the previous
+// segment's and are neither stored twice nor counted twice).
 template <int H>
 struct Geo {
     static constexpr int K = 2 * H + 1;
+    static constexpr int TY = tile_ty(H);
     static constexpr int IX = TX + 4 * H, IY = TY + 4 * H;
     static constexpr int AX = TX + 2 * H, AY = TY + 2 * H;
     static constexpr int NIN = IX * IY;
     static constexpr int J = cdiv(NIN, NT);               // input columns per lane
-    // forward x-pass: rows iy in [0,IY), SX outputs per item
-    static constexpr int SX = 4;
-    static constexpr int XSEG = cdiv(AX, SX);
-    static constexpr int XITEMS = IY * XSEG;
-    static constexpr int ZSTRIDE = odd(cmax(XSEG * SX + 2 * H, IX));
-    // forward y-pass: columns ax in [0,AX), SY outputs per item
-    static constexpr int SY = 4;
-    static constexpr int YSEG = cdiv(AY, SY);
-    static constexpr int YITEMS = AX * YSEG;
-    static constexpr int XROWS = cmax(IY, YSEG * SY + 2 * H);
-    static constexpr int XSTRIDE = odd(XSEG * SX);
-    // adjoint x-pass: rows ay in [0,AY), SX2 outputs per item
-    static constexpr int SX2 = 4;
-    static constexpr int X2SEG = TX / SX2;
-    static constexpr int X2ITEMS = AY * X2SEG;
-    static constexpr int GSTRIDE = odd(AX);
-    static constexpr int GXSTRIDE = odd(TX);
-    // adjoint y-pass + combine: one lane per (ox, pair of oy)
-    static_assert(TX * TY / 2 == NT, "combine stage maps one lane to two output columns");
-    // LDS plan (floats)
-    static constexpr int Z_FLOATS = 5 * IY * ZSTRIDE;
-    static constexpr int X_FLOATS = 5 * XROWS * XSTRIDE;
-    static constexpr int G_FLOATS = 3 * AY * GSTRIDE;
-    static constexpr int GX_FLOATS = 3 * AY * GXSTRIDE;
-    static constexpr int PT_FLOATS = 2 * 2 * TY * TX;
+    static constexpr int NOUT = TX * TY;                  // output columns (one lane each)
+    // X: x-sums of the five z-sums; items (iy, seg) over rows iy < IY, outputs ax < AX
+    static constexpr int SX = 8, XSEG = cdiv(AX, SX), XITEMS = IY * XSEG;
+    // Y: y-sums -> box sums, ncc, adjoints; items (ax, seg), outputs ay < AY
+    static constexpr int SY = 2, YSEG = cdiv(AY, SY), YITEMS = AX * YSEG;
+    // AX: x-sums of alpha, beta, gamma; items (ay, seg), outputs ox < TX
+    static constexpr int SA = 8, ASEG = TX / SA, AITEMS = AY * ASEG;
+    // AYs: y-sums of the three; items (ox, seg), outputs oy < TY
+    static constexpr int SB = 8, BSEG = TY / SB, BITEMS = TX * BSEG;
+    // lane ranges of the stages sharing a phase (wave-aligned, disjoint)
+    static constexpr int Y_OFF = 0, B_OFF = 768;
+    static constexpr int X_OFF = 512, A_OFF = X_OFF + rup64(XITEMS);
+    static_assert(YITEMS <= B_OFF && B_OFF + BITEMS <= NT && A_OFF + AITEMS <= NT, "lanes");
+    static_assert(AX >= SX && AY >= SY && TX % SA == 0 && TY % SB == 0, "segments");
+    // LDS layout (floats): Zs[5][IY][ZS], XsT[5][AX][XS] (transposed), Gs[3][AY][GS],
+    // GXsT[3][TX][GXS] (transposed), GY[3][TY][GYS]
+    static constexpr int ZS = stride2(IX), XS = stride2(IY), GS = stride2(AX), GXS = stride2(AY);
+    static constexpr int GYS = TX + 1;
+    static constexpr int ZP = IY * ZS, XP = AX * XS, GP = AY * GS, GXP = TX * GXS, GYP = TY * GYS;
+    static constexpr int Z_OFF = 0, XS_OFF = 5 * ZP, G_OFF = XS_OFF + 5 * XP, GX_OFF = G_OFF + 3 * GP;
+    static constexpr int GY_OFF = GX_OFF + 3 * GXP;
+    static constexpr int LDS_FLOATS = GY_OFF + 3 * GYP;
+    static constexpr int LDS_FLOATS_LOSS = XS_OFF + 5 * XP;  // forward-only modes
+    static_assert(LDS_FLOATS * 4 <= 160 * 1024, "LDS");
 };
 
 }  // namespace fl

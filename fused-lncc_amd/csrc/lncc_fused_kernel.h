@@ -1,20 +1,26 @@
 // Fused 3D LNCC kernels for gfx950 (MI355X).
 //
-// One workgroup owns a TX x TY tile of output columns of one (D,H,W) volume and marches along D
-// over a chunk [z0,z1) of planes. For each input plane zi it runs a software pipeline whose stages
-// are lagged along D, so that every quantity is produced from data already on chip:
+// One workgroup (1024 lanes) owns a TX x TY tile of output columns of one (D,H,W) volume and
+// marches along D over a chunk [z0,z1) of planes. Per input plane zi it runs six stages, lagged
+// along D so that every quantity is produced from data already on chip:
 //
-//   F  (registers) each lane owns input columns of the (TX+4h) x (TY+4h) region; it loads p,t of
-//      plane zi (prefetched one plane ahead), keeps a k-deep ring of raw p,t and running z-sums of
-//      p, t, p^2, t^2, p*t, and writes the five z-sums of the plane to LDS.
-//   X  (LDS) running x-sums of the five z-sums over the (TX+2h)-wide adjoint range.
-//   Y  (LDS) running y-sums -> the five k^3 box-sums at plane zc = zi-h on the (TX+2h) x (TY+2h)
-//      adjoint region; per voxel squared NCC (clamped to 1) and the three adjoint coefficients
-//      alpha, beta, gamma (zero where ncc >= 1 or outside the volume); loss partial sums.
-//   AX (LDS) running x-sums of alpha, beta, gamma over the TX output columns.
-//   AY (registers) running y-sums for two output rows per lane, a k-deep ring of the xy-sums and
-//      running z-sums -> box(alpha), box(beta), box(gamma) at plane zo = zi-2h, combined with p,t
-//      of plane zo into the gradient, which is the only per-voxel write to HBM.
+//   F   (registers) lanes own the input columns of the (TX+4h) x (TY+4h) region and keep running
+//       z-sums of p, t, p^2, t^2, p*t: add plane zi, subtract plane zi-k (re-read from global
+//       memory, where it is still cache-resident, rather than held in a register ring; both are
+//       prefetched one plane ahead); write the five z-sums to LDS.
+//   X   running x-sums of the five z-sums over the (TX+2h)-wide adjoint range.
+//   Y   running y-sums -> the five k^3 box-sums on the (TX+2h) x (TY+2h) adjoint region; per voxel
+//       squared NCC (clamped to 1), loss partial sums, and the adjoint coefficients alpha, beta,
+//       gamma (zero where ncc >= 1 or outside the volume).
+//   AX  running x-sums of alpha, beta, gamma over the TX output columns.
+//   AYs running y-sums of the three over the TY output rows.
+//   AZ  (registers) one lane per output column: k-deep ring of the xy-sums and running z-sums ->
+//       box(alpha), box(beta), box(gamma), combined with p,t of the output plane (re-read, cache
+//       resident) into the gradient, the only per-voxel write to HBM.
+//
+// Software pipeline: the chain F -> X -> Y -> AX -> AYs -> AZ alternates between two phases per
+// plane, P0 = {F(zi), Y(zi-1), AYs(zi-2)} and P1 = {X(zi), AX(zi-1), AZ(zi-2)}, so each plane costs
+// two workgroup barriers, and the stages that share a phase run on disjoint waves.
 //
 // Reference semantics (fused_lncc/csrc/lncc3d.cu:93-107, baselines/torch_lncc.py:25-32):
 //   cross = Spt - Sp St/n ; vp = max(Spp - Sp^2/n, 0) + dr ; vt likewise ; ncc = cross^2/(vp vt);
@@ -29,6 +35,27 @@
 
 namespace fl {
 
+// Running window sums of width 2H+1 over S consecutive outputs from S+2H inputs read as float2.
+template <int H, int S>
+__device__ __forceinline__ void window_sums(const float* __restrict__ src, float (&out)[S]) {
+    float v[S + 2 * H];
+#pragma unroll
+    for (int m = 0; m < (S + 2 * H) / 2; ++m) {
+        const float2 f = reinterpret_cast<const float2*>(src)[m];
+        v[2 * m] = f.x;
+        v[2 * m + 1] = f.y;
+    }
+    float acc = v[0];
+#pragma unroll
+    for (int i = 1; i <= 2 * H; ++i) acc += v[i];
+    out[0] = acc;
+#pragma unroll
+    for (int i = 1; i < S; ++i) {
+        acc += v[i + 2 * H] - v[i - 1];
+        out[i] = acc;
+    }
+}
+
 template <int HH, bool BF16, int MODE>
 __global__ __launch_bounds__(NT, 1) void lncc_fused_kernel(FusedArgs a) {
     using G = Geo<HH>;
@@ -36,18 +63,15 @@ __global__ __launch_bounds__(NT, 1) void lncc_fused_kernel(FusedArgs a) {
     constexpr bool ADJ = (MODE == MODE_GRAD);
     constexpr int ELEM = BF16 ? 2 : 4;
     constexpr int J = G::J;
-    constexpr int ZP = G::IY * G::ZSTRIDE;
-    constexpr int XP = G::XROWS * G::XSTRIDE;
-    constexpr int GP = G::AY * G::GSTRIDE;
-    constexpr int GXP = G::AY * G::GXSTRIDE;
-    constexpr int PTP = TY * TX;
+    constexpr int TY = G::TY;
 
-    __shared__ float zs[G::Z_FLOATS];
-    __shared__ float xs[G::X_FLOATS];
-    __shared__ float gs[ADJ ? G::G_FLOATS : 1];
-    __shared__ float gxs[ADJ ? G::GX_FLOATS : 1];
-    __shared__ float pts[ADJ ? G::PT_FLOATS : 1];
+    __shared__ __align__(16) float lds[ADJ ? G::LDS_FLOATS : G::LDS_FLOATS_LOSS];
     __shared__ double red[NT / 64];
+    float* const Zs = lds + G::Z_OFF;
+    float* const Xs = lds + G::XS_OFF;
+    float* const Gs = lds + G::G_OFF;
+    float* const GXs = lds + G::GX_OFF;
+    float* const GY = lds + G::GY_OFF;
 
     const int tid = threadIdx.x;
     const int D = a.dimD, Hd = a.dimH, Wd = a.dimW;
@@ -66,45 +90,62 @@ __global__ __launch_bounds__(NT, 1) void lncc_fused_kernel(FusedArgs a) {
     const char* pvol = (const char*)a.pred + b * D * HW * ELEM;
     const char* tvol = (const char*)a.target + b * D * HW * ELEM;
 
-    for (int i = tid; i < G::Z_FLOATS; i += NT) zs[i] = 0.f;
-    for (int i = tid; i < G::X_FLOATS; i += NT) xs[i] = 0.f;
-    if constexpr (ADJ) {
-        for (int i = tid; i < G::G_FLOATS; i += NT) gs[i] = 0.f;
-        for (int i = tid; i < G::GX_FLOATS; i += NT) gxs[i] = 0.f;
-    }
-
-    // ---- per-lane input columns
+    // ---- F: per-lane input columns
     uint32_t voff[J];
-    int zoff[J], ptoff[J];
+    int zaddr[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int c = tid + j * NT;
         voff[j] = kOOB;
-        zoff[j] = -1;
-        ptoff[j] = -1;
+        zaddr[j] = -1;
         if (c < G::NIN) {
             const int iy = c / G::IX, ix = c - iy * G::IX;
             const int gx = x0 - 2 * HH + ix, gy = y0 - 2 * HH + iy;
             if (gx >= 0 && gx < Wd && gy >= 0 && gy < Hd) voff[j] = (uint32_t)((gy * Wd + gx) * ELEM);
-            zoff[j] = iy * G::ZSTRIDE + ix;
-            const int cx = ix - 2 * HH, cy = iy - 2 * HH;
-            if (cx >= 0 && cx < TX && cy >= 0 && cy < TY) ptoff[j] = cy * TX + cx;
+            zaddr[j] = iy * G::ZS + ix;
         }
     }
+    // ---- per-lane items of the segment stages (at most one per stage)
+    const int yi = tid - G::Y_OFF;
+    const bool has_y = yi >= 0 && yi < G::YITEMS;
+    const int y_ax = has_y ? yi % G::AX : 0;
+    const int y_seg = has_y ? yi / G::AX : 0;
+    const int y_start = min(y_seg * G::SY, G::AY - G::SY);
+    const int y_fresh = y_seg * G::SY - y_start;
+    const int xi = tid - G::X_OFF;
+    const bool has_x = xi >= 0 && xi < G::XITEMS;
+    const int x_iy = has_x ? xi % G::IY : 0;
+    const int x_seg = has_x ? xi / G::IY : 0;
+    const int x_start = min(x_seg * G::SX, G::AX - G::SX);
+    const int x_fresh = x_seg * G::SX - x_start;
+    const int ai = tid - G::A_OFF;
+    const bool has_a = ADJ && ai >= 0 && ai < G::AITEMS;
+    const int a_ay = has_a ? ai % G::AY : 0;
+    const int a_start = has_a ? (ai / G::AY) * G::SA : 0;
+    const int bi = tid - G::B_OFF;
+    const bool has_b = ADJ && bi >= 0 && bi < G::BITEMS;
+    const int b_ox = has_b ? bi % TX : 0;
+    const int b_start = has_b ? (bi / TX) * G::SB : 0;
+    const bool has_z = ADJ && tid < G::NOUT;
+    const int z_ox = tid % TX, z_oy = tid / TX;
+    const bool z_in = has_z && x0 + z_ox < Wd && y0 + z_oy < Hd;
+    const uint32_t z_voff = z_in ? (uint32_t)(((y0 + z_oy) * Wd + x0 + z_ox) * ELEM) : kOOB;
 
     constexpr int LEAD = ADJ ? 2 * HH : HH;
     const int zlo = max(z0 - LEAD, 0);
-    const int zhi = z1 + LEAD;
+    const int zhi = ADJ ? z1 + 2 + 2 * HH : z1 + 1 + HH;
     const int zc_lo = ADJ ? max(z0 - HH, 0) : z0;
     const int zc_hi = ADJ ? min(z1 + HH, D) : z1;
 
-    float pring[J][K], tring[J][K], zsum[J][5], pnext[J], tnext[J];
+    // F state: running z-sums; p,t of the next plane and of the plane leaving the window (prefetched)
+    float zsum[J][5], pnext[J], tnext[J], pold[J], told[J];
+    float pz = 0.f, tzz = 0.f;  // AZ: p,t at the next step's output plane (prefetched)
 #pragma unroll
     for (int j = 0; j < J; ++j) {
 #pragma unroll
-        for (int r = 0; r < K; ++r) { pring[j][r] = 0.f; tring[j][r] = 0.f; }
-#pragma unroll
         for (int q = 0; q < 5; ++q) zsum[j][q] = 0.f;
+        pold[j] = 0.f;
+        told[j] = 0.f;
     }
     {
         const __amdgpu_buffer_rsrc_t rp = make_rsrc(pvol + (int64_t)zlo * HW * ELEM, plane_bytes);
@@ -115,248 +156,202 @@ __global__ __launch_bounds__(NT, 1) void lncc_fused_kernel(FusedArgs a) {
             tnext[j] = load_elem<BF16>(rt, voff[j]);
         }
     }
-
-    // adjoint-side state: lane owns output columns (ox, oy) and (ox, oy+1)
-    const int ox = tid % TX;
-    const int oy = 2 * (tid / TX);
-    float gring[2][3][K], gz[2][3];
+    float gring[3][K], gz[3];
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+    for (int c = 0; c < 3; ++c) {
+        gz[c] = 0.f;
 #pragma unroll
-        for (int c = 0; c < 3; ++c) {
-            gz[m][c] = 0.f;
-#pragma unroll
-            for (int r = 0; r < K; ++r) gring[m][c][r] = 0.f;
-        }
+        for (int r = 0; r < K; ++r) gring[c][r] = 0.f;
+    }
 
     double loss_acc = 0.0;
     const float inv_n = a.inv_n, dr = a.dr;
-    __syncthreads();
 
     for (int base = zlo; base < zhi; base += K) {
         static_for<0, K>([&](auto rc) __attribute__((always_inline)) {
             constexpr int r = decltype(rc)::value;
             const int zi = base + r;
             if (zi >= zhi) return;
-            const int s = zi - zlo;
 
-            // ---------------- F: z-sums of the input region ----------------
-            float pc[J], tc[J];
-#pragma unroll
-            for (int j = 0; j < J; ++j) { pc[j] = pnext[j]; tc[j] = tnext[j]; }
-            if (zi + 1 < zhi && zi + 1 < D) {
-                const __amdgpu_buffer_rsrc_t rp = make_rsrc(pvol + (int64_t)(zi + 1) * HW * ELEM, plane_bytes);
-                const __amdgpu_buffer_rsrc_t rt = make_rsrc(tvol + (int64_t)(zi + 1) * HW * ELEM, plane_bytes);
+            // ============================ phase P0 ============================
+            float pzcur, tzcur;  // p,t at this step's output plane
+            // F(zi): z-sums of the input region
+            {
+                float pc[J], tc[J], po[J], to[J];
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
-                    pnext[j] = load_elem<BF16>(rp, voff[j]);
-                    tnext[j] = load_elem<BF16>(rt, voff[j]);
+                    pc[j] = pnext[j];
+                    tc[j] = tnext[j];
+                    po[j] = pold[j];
+                    to[j] = told[j];
                 }
-            } else {
+                const float pzc = pz, tzc = tzz;
+                // prefetch plane zi+1, plane zi+1-k (leaving the window) and the output plane of step+1
+                const int zn = zi + 1, zq = zi + 1 - K, zon = zi - 1 - 2 * HH;
+                if (zn < zhi && zn < D) {
+                    const __amdgpu_buffer_rsrc_t rp = make_rsrc(pvol + (int64_t)zn * HW * ELEM, plane_bytes);
+                    const __amdgpu_buffer_rsrc_t rt = make_rsrc(tvol + (int64_t)zn * HW * ELEM, plane_bytes);
 #pragma unroll
-                for (int j = 0; j < J; ++j) { pnext[j] = 0.f; tnext[j] = 0.f; }
-            }
-            constexpr int ro = (r + 1) % K;  // oldest ring slot after this step: plane zi-2h
+                    for (int j = 0; j < J; ++j) {
+                        pnext[j] = load_elem<BF16>(rp, voff[j]);
+                        tnext[j] = load_elem<BF16>(rt, voff[j]);
+                    }
+                } else {
 #pragma unroll
-            for (int j = 0; j < J; ++j) {
-                const float p = pc[j], t = tc[j];
-                const float po = pring[j][r], to = tring[j][r];
-                zsum[j][0] += p - po;
-                zsum[j][1] += t - to;
-                zsum[j][2] = fmaf(p, p, fmaf(-po, po, zsum[j][2]));
-                zsum[j][3] = fmaf(t, t, fmaf(-to, to, zsum[j][3]));
-                zsum[j][4] = fmaf(p, t, fmaf(-po, to, zsum[j][4]));
-                pring[j][r] = p;
-                tring[j][r] = t;
-                if (zoff[j] >= 0) {
+                    for (int j = 0; j < J; ++j) { pnext[j] = 0.f; tnext[j] = 0.f; }
+                }
+                if (zq >= zlo && zq < D && zn < zhi) {
+                    const __amdgpu_buffer_rsrc_t rp = make_rsrc(pvol + (int64_t)zq * HW * ELEM, plane_bytes);
+                    const __amdgpu_buffer_rsrc_t rt = make_rsrc(tvol + (int64_t)zq * HW * ELEM, plane_bytes);
 #pragma unroll
-                    for (int q = 0; q < 5; ++q) zs[q * ZP + zoff[j]] = zsum[j][q];
+                    for (int j = 0; j < J; ++j) {
+                        pold[j] = load_elem<BF16>(rp, voff[j]);
+                        told[j] = load_elem<BF16>(rt, voff[j]);
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < J; ++j) { pold[j] = 0.f; told[j] = 0.f; }
                 }
                 if constexpr (ADJ) {
-                    if (ptoff[j] >= 0) {
-                        pts[(s & 1) * 2 * PTP + ptoff[j]] = pring[j][ro];
-                        pts[(s & 1) * 2 * PTP + PTP + ptoff[j]] = tring[j][ro];
+                    if (zon >= z0 && zon < z1) {
+                        const __amdgpu_buffer_rsrc_t rp = make_rsrc(pvol + (int64_t)zon * HW * ELEM, plane_bytes);
+                        const __amdgpu_buffer_rsrc_t rt = make_rsrc(tvol + (int64_t)zon * HW * ELEM, plane_bytes);
+                        pz = load_elem<BF16>(rp, z_voff);
+                        tzz = load_elem<BF16>(rt, z_voff);
                     }
                 }
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    const float p = pc[j], t = tc[j];
+                    zsum[j][0] += p - po[j];
+                    zsum[j][1] += t - to[j];
+                    zsum[j][2] = fmaf(p, p, fmaf(-po[j], po[j], zsum[j][2]));
+                    zsum[j][3] = fmaf(t, t, fmaf(-to[j], to[j], zsum[j][3]));
+                    zsum[j][4] = fmaf(p, t, fmaf(-po[j], to[j], zsum[j][4]));
+                    if (zaddr[j] >= 0) {
+#pragma unroll
+                        for (int q = 0; q < 5; ++q) Zs[q * G::ZP + zaddr[j]] = zsum[j][q];
+                    }
+                }
+                pzcur = pzc;
+                tzcur = tzc;
             }
-            __syncthreads();
-
-            const int zc = zi - HH;
-            const bool fwd = (zc >= zc_lo) && (zc < zc_hi);
-            if (fwd) {
-                // ---------------- X: running x-sums of the five z-sums ----------------
+            // Y(zi-1): box sums, ncc, adjoint coefficients at plane zcY
+            const int zcY = zi - 1 - HH;
+            const bool actY = zcY >= zc_lo && zcY < zc_hi;
+            if (actY && has_y) {
+                float S[5][G::SY];
 #pragma unroll
-                for (int u = 0; u < cdiv(G::XITEMS, NT); ++u) {
-                    const int it = tid + u * NT;
-                    if (it < G::XITEMS) {
-                        const int iy = it % G::IY, seg = it / G::IY;
-                        const float* src = zs + iy * G::ZSTRIDE + seg * G::SX;
-                        float* dst = xs + iy * G::XSTRIDE + seg * G::SX;
-#pragma unroll
-                        for (int q = 0; q < 5; ++q) {
-                            float v[G::SX + 2 * HH];
-#pragma unroll
-                            for (int i = 0; i < G::SX + 2 * HH; ++i) v[i] = src[q * ZP + i];
-                            float acc = v[0];
-#pragma unroll
-                            for (int i = 1; i <= 2 * HH; ++i) acc += v[i];
-                            dst[q * XP] = acc;
-#pragma unroll
-                            for (int i = 1; i < G::SX; ++i) {
-                                acc += v[i + 2 * HH] - v[i - 1];
-                                dst[q * XP + i] = acc;
-                            }
-                        }
-                    }
-                }
-                __syncthreads();
-
-                // ---------------- Y: box-sums, ncc, adjoint coefficients ----------------
-                const bool count = (zc >= z0) && (zc < z1);
+                for (int q = 0; q < 5; ++q) window_sums<HH, G::SY>(Xs + q * G::XP + y_ax * G::XS + y_start, S[q]);
+                const int gx = x0 - HH + y_ax;
+                const bool inx = gx >= 0 && gx < Wd;
+                const bool corex = y_ax >= HH && y_ax < HH + TX;
+                const bool count = zcY >= z0 && zcY < z1;
                 float lsum = 0.f;
 #pragma unroll
-                for (int u = 0; u < cdiv(G::YITEMS, NT); ++u) {
-                    const int it = tid + u * NT;
-                    if (it < G::YITEMS) {
-                        const int ax = it % G::AX, seg = it / G::AX;
-                        const float* src = xs + seg * G::SY * G::XSTRIDE + ax;
-                        float S[5][G::SY];
-#pragma unroll
-                        for (int q = 0; q < 5; ++q) {
-                            float v[G::SY + 2 * HH];
-#pragma unroll
-                            for (int i = 0; i < G::SY + 2 * HH; ++i) v[i] = src[q * XP + i * G::XSTRIDE];
-                            float acc = v[0];
-#pragma unroll
-                            for (int i = 1; i <= 2 * HH; ++i) acc += v[i];
-                            S[q][0] = acc;
-#pragma unroll
-                            for (int i = 1; i < G::SY; ++i) {
-                                acc += v[i + 2 * HH] - v[i - 1];
-                                S[q][i] = acc;
-                            }
+                for (int i = 0; i < G::SY; ++i) {
+                    const int ay = y_start + i;
+                    const bool fresh = i >= y_fresh;
+                    const float Sp = S[0][i], St = S[1][i], Spp = S[2][i], Stt = S[3][i], Spt = S[4][i];
+                    const float mp = Sp * inv_n, mt = St * inv_n;
+                    const float cross = fmaf(-mp, St, Spt);
+                    const float vp = fmaxf(fmaf(-mp, Sp, Spp), 0.f) + dr;
+                    const float vt = fmaxf(fmaf(-mt, St, Stt), 0.f) + dr;
+                    const float rr = __builtin_amdgcn_rcpf(vp * vt);
+                    const float cr = cross * rr;
+                    const float ncc = cross * cr;
+                    const int gy = y0 - HH + ay;
+                    const bool inv = inx && gy >= 0 && gy < Hd;
+                    const bool live = inv && (ncc < 1.0f);
+                    const float nccc = (ncc >= 1.0f) ? 1.0f : ncc;
+                    const bool core = corex && ay >= HH && ay < HH + TY;
+                    if (count && inv && core && fresh) lsum += nccc;
+                    if constexpr (ADJ) {
+                        const float uu = cr * vt;
+                        const float w = fmaf(-Sp, uu, St);
+                        if (fresh) {
+                            Gs[0 * G::GP + ay * G::GS + y_ax] = live ? cr * w : 0.f;
+                            Gs[1 * G::GP + ay * G::GS + y_ax] = live ? cr * uu : 0.f;
+                            Gs[2 * G::GP + ay * G::GS + y_ax] = live ? cr : 0.f;
                         }
-                        const int gx = x0 - HH + ax;
-                        const bool inx = gx >= 0 && gx < Wd;
-                        const bool corex = ax >= HH && ax < HH + TX;
-#pragma unroll
-                        for (int i = 0; i < G::SY; ++i) {
-                            const int ay = seg * G::SY + i;
-                            const float Sp = S[0][i], St = S[1][i], Spp = S[2][i], Stt = S[3][i], Spt = S[4][i];
-                            const float mp = Sp * inv_n, mt = St * inv_n;
-                            const float cross = fmaf(-mp, St, Spt);
-                            const float vp = fmaxf(fmaf(-mp, Sp, Spp), 0.f) + dr;
-                            const float vt = fmaxf(fmaf(-mt, St, Stt), 0.f) + dr;
-                            const float rr = __builtin_amdgcn_rcpf(vp * vt);
-                            const float cr = cross * rr;
-                            const float ncc = cross * cr;
-                            const int gy = y0 - HH + ay;
-                            const bool inv = inx && gy >= 0 && gy < Hd && ay < G::AY;
-                            const bool live = inv && (ncc < 1.0f);
-                            const float nccc = (ncc >= 1.0f) ? 1.0f : ncc;
-                            const bool core = corex && ay >= HH && ay < HH + TY;
-                            if (count && inv && core) lsum += nccc;
-                            if constexpr (ADJ) {
-                                const float uu = cr * vt;
-                                const float w = fmaf(-Sp, uu, St);
-                                if (ay < G::AY) {
-                                    gs[0 * GP + ay * G::GSTRIDE + ax] = live ? cr * w : 0.f;
-                                    gs[1 * GP + ay * G::GSTRIDE + ax] = live ? cr * uu : 0.f;
-                                    gs[2 * GP + ay * G::GSTRIDE + ax] = live ? cr : 0.f;
-                                }
-                            }
-                            if constexpr (MODE == MODE_MAPS) {
-                                if (count && inv && core) {
-                                    const float uu = cr * vt;
-                                    const float w = fmaf(-Sp, uu, St);
-                                    const int64_t o = ((b * D + zc) * Hd + gy) * (int64_t)Wd + gx;
-                                    a.ncc_map[o] = nccc;
-                                    a.a_map[o] = live ? -2.f * inv_n * (cr * w) : 0.f;
-                                    a.b_map[o] = live ? -(cr * uu) : 0.f;
-                                    a.c_map[o] = live ? 2.f * cr : 0.f;
-                                }
-                            }
+                    }
+                    if constexpr (MODE == MODE_MAPS) {
+                        if (count && inv && core && fresh) {
+                            const float uu = cr * vt;
+                            const float w = fmaf(-Sp, uu, St);
+                            const int64_t o = ((b * D + zcY) * Hd + gy) * (int64_t)Wd + gx;
+                            a.ncc_map[o] = nccc;
+                            a.a_map[o] = live ? -2.f * inv_n * (cr * w) : 0.f;
+                            a.b_map[o] = live ? -(cr * uu) : 0.f;
+                            a.c_map[o] = live ? 2.f * cr : 0.f;
                         }
                     }
                 }
                 loss_acc += (double)lsum;
             }
-
+            // AYs(zi-2): y-sums of alpha, beta, gamma at plane zcB
+            const int zcB = zi - 2 - HH;
+            const bool actB = ADJ && zcB >= zc_lo && zcB < zc_hi;
             if constexpr (ADJ) {
-                if (fwd) {
-                    __syncthreads();
-                    // ---------------- AX: running x-sums of alpha, beta, gamma ----------------
-#pragma unroll
-                    for (int u = 0; u < cdiv(G::X2ITEMS, NT); ++u) {
-                        const int it = tid + u * NT;
-                        if (it < G::X2ITEMS) {
-                            const int ay = it % G::AY, seg = it / G::AY;
-                            const float* src = gs + ay * G::GSTRIDE + seg * G::SX2;
-                            float* dst = gxs + ay * G::GXSTRIDE + seg * G::SX2;
-#pragma unroll
-                            for (int c = 0; c < 3; ++c) {
-                                float v[G::SX2 + 2 * HH];
-#pragma unroll
-                                for (int i = 0; i < G::SX2 + 2 * HH; ++i) v[i] = src[c * GP + i];
-                                float acc = v[0];
-#pragma unroll
-                                for (int i = 1; i <= 2 * HH; ++i) acc += v[i];
-                                dst[c * GXP] = acc;
-#pragma unroll
-                                for (int i = 1; i < G::SX2; ++i) {
-                                    acc += v[i + 2 * HH] - v[i - 1];
-                                    dst[c * GXP + i] = acc;
-                                }
-                            }
-                        }
-                    }
-                    __syncthreads();
-                }
-                // ---------------- AY: y-sums, z ring, combine ----------------
-                float ys[2][3];
-                if (fwd) {
-                    const float* src = gxs + oy * G::GXSTRIDE + ox;
+                if (actB && has_b) {
 #pragma unroll
                     for (int c = 0; c < 3; ++c) {
-                        float v[2 + 2 * HH];
+                        float o[G::SB];
+                        window_sums<HH, G::SB>(GXs + c * G::GXP + b_ox * G::GXS + b_start, o);
 #pragma unroll
-                        for (int i = 0; i < 2 + 2 * HH; ++i) v[i] = src[c * GXP + i * G::GXSTRIDE];
-                        float acc = v[0];
-#pragma unroll
-                        for (int i = 1; i <= 2 * HH; ++i) acc += v[i];
-                        ys[0][c] = acc;
-                        ys[1][c] = acc + v[2 * HH + 1] - v[0];
-                    }
-                } else {
-#pragma unroll
-                    for (int m = 0; m < 2; ++m)
-#pragma unroll
-                        for (int c = 0; c < 3; ++c) ys[m][c] = 0.f;
-                }
-#pragma unroll
-                for (int m = 0; m < 2; ++m)
-#pragma unroll
-                    for (int c = 0; c < 3; ++c) {
-                        gz[m][c] += ys[m][c] - gring[m][c][r];
-                        gring[m][c][r] = ys[m][c];
-                    }
-                const int zo = zi - 2 * HH;
-                if (zo >= z0 && zo < z1) {
-                    const int gx = x0 + ox;
-#pragma unroll
-                    for (int m = 0; m < 2; ++m) {
-                        const int gy = y0 + oy + m;
-                        const float p = pts[(s & 1) * 2 * PTP + (oy + m) * TX + ox];
-                        const float t = pts[(s & 1) * 2 * PTP + PTP + (oy + m) * TX + ox];
-                        const float g = a.gscale * fmaf(inv_n, gz[m][0], fmaf(p, gz[m][1], -t * gz[m][2]));
-                        if (gx < Wd && gy < Hd) store_elem<BF16>(a.grad, ((b * D + zo) * Hd + gy) * (int64_t)Wd + gx, g);
+                        for (int i = 0; i < G::SB; ++i) GY[c * G::GYP + (b_start + i) * G::GYS + b_ox] = o[i];
                     }
                 }
             }
+            __syncthreads();
+
+            // ============================ phase P1 ============================
+            // X(zi): x-sums of the z-sums (feeds Y at the next plane)
+            const int zcX = zi - HH;
+            if (zcX >= zc_lo && zcX < zc_hi && has_x) {
+#pragma unroll
+                for (int q = 0; q < 5; ++q) {
+                    float o[G::SX];
+                    window_sums<HH, G::SX>(Zs + q * G::ZP + x_iy * G::ZS + x_start, o);
+#pragma unroll
+                    for (int i = 0; i < G::SX; ++i)
+                        if (i >= x_fresh) Xs[q * G::XP + (x_start + i) * G::XS + x_iy] = o[i];
+                }
+            }
+            if constexpr (ADJ) {
+                // AX(zi-1): x-sums of alpha, beta, gamma at plane zcY
+                if (actY && has_a) {
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) {
+                        float o[G::SA];
+                        window_sums<HH, G::SA>(Gs + c * G::GP + a_ay * G::GS + a_start, o);
+#pragma unroll
+                        for (int i = 0; i < G::SA; ++i) GXs[c * G::GXP + (a_start + i) * G::GXS + a_ay] = o[i];
+                    }
+                }
+                // AZ(zi-2): z ring of the xy-sums, combine at the output plane zo
+                if (has_z) {
+                    float ys[3];
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) ys[c] = actB ? GY[c * G::GYP + z_oy * G::GYS + z_ox] : 0.f;
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) {
+                        gz[c] += ys[c] - gring[c][r];
+                        gring[c][r] = ys[c];
+                    }
+                    const int zo = zcB - HH;
+                    const int gx = x0 + z_ox, gy = y0 + z_oy;
+                    if (zo >= z0 && zo < z1 && gx < Wd && gy < Hd) {
+                        const float g = a.gscale * fmaf(inv_n, gz[0], fmaf(pzcur, gz[1], -tzcur * gz[2]));
+                        store_elem<BF16>(a.grad, ((b * D + zo) * Hd + gy) * (int64_t)Wd + gx, g);
+                    }
+                }
+            }
+            __syncthreads();
         });
     }
 
-    // ---- workgroup partial of the ncc sum: wave64 reduction, then the 8 waves in fixed order
+    // ---- workgroup partial of the ncc sum: wave64 reduction, then the 16 waves in fixed order
     if constexpr (MODE == MODE_MAPS) return;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) loss_acc += __shfl_xor(loss_acc, off, 64);
