@@ -8,8 +8,10 @@
 
 namespace fl {
 
-// Workgroup: 1024 lanes (16 wave64s). Output tile: TX x TY columns of one volume, marched along D.
+// Workgroup: 1024 lanes (16 wave64s, one workgroup per CU). Output tile: TX x TY columns of one
+// volume, marched along D.
 constexpr int NT = 1024;
+constexpr int WG_PER_CU = 1;
 constexpr int TX = 32;
 constexpr __host__ __device__ inline int tile_ty(int halo) { return halo == 4 ? 24 : 32; }
 
@@ -20,6 +22,14 @@ constexpr uint32_t kOOB = 0x80000000u;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+
+// Resource for plane z (clamped into [0, D)) of a volume; `valid == false` gives a zero-sized
+// buffer, so loads through it return 0 and stores through it are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void* vol, int z, int D, int64_t plane_bytes,
+                                                               bool valid) {
+    const int zc = z < 0 ? 0 : (z >= D ? D - 1 : z);
+    return make_rsrc((const char*)vol + (int64_t)zc * plane_bytes, valid ? (uint32_t)plane_bytes : 0u);
 }
 
 template <bool BF16>
@@ -48,6 +58,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
     if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
     u += 0x7fffu + ((u >> 16) & 1u);
     return (uint16_t)(u >> 16);
+}
+
+template <bool BF16>
+__device__ __forceinline__ void store_elem_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, float v) {
+    if constexpr (BF16) {
+        __builtin_amdgcn_raw_buffer_store_b16((unsigned short)f32_to_bf16_bits(v), r, (int)voff, 0, 0);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)voff, 0, 0);
+    }
 }
 
 template <bool BF16>
@@ -102,14 +121,17 @@ struct Geo {
     static constexpr int SA = 8, ASEG = TX / SA, AITEMS = AY * ASEG;
     // AYs: y-sums of the three; items (ox, seg), outputs oy < TY
     static constexpr int SB = 8, BSEG = TY / SB, BITEMS = TX * BSEG;
-    // lane ranges of the stages sharing a phase (wave-aligned, disjoint)
-    static constexpr int Y_OFF = 0, B_OFF = 768;
-    static constexpr int X_OFF = 512, A_OFF = X_OFF + rup64(XITEMS);
-    static_assert(YITEMS <= B_OFF && B_OFF + BITEMS <= NT && A_OFF + AITEMS <= NT, "lanes");
+    // Work units of the running-sum passes are single quantities of one segment, spread over all
+    // lanes: phase P1 runs the X units (5 per item) then the AX units (3 per item); phase P0 runs
+    // Y items on the first lanes and the AYs units (3 per item) on the last lanes.
+    static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, U1 = cdiv(UX + UA, NT);
+    static constexpr int UB = 3 * BITEMS, B_LANE0 = NT - UB;
+    static_assert(YITEMS <= NT && UB <= NT && SX == SA, "lanes");
     static_assert(AX >= SX && AY >= SY && TX % SA == 0 && TY % SB == 0, "segments");
     // LDS layout (floats): Zs[5][IY][ZS], XsT[5][AX][XS] (transposed), Gs[3][AY][GS],
     // GXsT[3][TX][GXS] (transposed), GY[3][TY][GYS]
-    static constexpr int ZS = stride2(IX), XS = stride2(IY), GS = stride2(AX), GXS = stride2(AY);
+    // XS == GXS: the X and AX passes share one code path (same destination stride)
+    static constexpr int ZS = stride2(IX), XS = stride2(cmax(IY, AY)), GS = stride2(AX), GXS = XS;
     static constexpr int GYS = TX + 1;
     static constexpr int ZP = IY * ZS, XP = AX * XS, GP = AY * GS, GXP = TX * GXS, GYP = TY * GYS;
     static constexpr int Z_OFF = 0, XS_OFF = 5 * ZP, G_OFF = XS_OFF + 5 * XP, GX_OFF = G_OFF + 3 * GP;

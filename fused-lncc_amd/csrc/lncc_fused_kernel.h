@@ -57,7 +57,7 @@ __device__ __forceinline__ void window_sums(const float* __restrict__ src, float
 }
 
 template <int HH, bool BF16, int MODE>
-__global__ __launch_bounds__(NT, 1) void lncc_fused_kernel(FusedArgs a) {
+__global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) {
     using G = Geo<HH>;
     constexpr int K = G::K;
     constexpr bool ADJ = (MODE == MODE_GRAD);
@@ -65,13 +65,14 @@ __global__ __launch_bounds__(NT, 1) void lncc_fused_kernel(FusedArgs a) {
     constexpr int J = G::J;
     constexpr int TY = G::TY;
 
-    __shared__ __align__(16) float lds[ADJ ? G::LDS_FLOATS : G::LDS_FLOATS_LOSS];
+    // one __shared__ array per buffer, so the compiler knows that the reads of one stage do not
+    // alias the writes of another and can overlap them
+    __shared__ __align__(16) float Zs[5 * G::ZP];
+    __shared__ __align__(16) float Xs[5 * G::XP];
+    __shared__ __align__(16) float Gs[ADJ ? 3 * G::GP : 2];
+    __shared__ __align__(16) float GXs[ADJ ? 3 * G::GXP : 2];
+    __shared__ __align__(16) float GY[ADJ ? 3 * G::GYP : 2];
     __shared__ double red[NT / 64];
-    float* const Zs = lds + G::Z_OFF;
-    float* const Xs = lds + G::XS_OFF;
-    float* const Gs = lds + G::G_OFF;
-    float* const GXs = lds + G::GX_OFF;
-    float* const GY = lds + G::GY_OFF;
 
     const int tid = threadIdx.x;
     const int D = a.dimD, Hd = a.dimH, Wd = a.dimW;
@@ -89,6 +90,7 @@ __global__ __launch_bounds__(NT, 1) void lncc_fused_kernel(FusedArgs a) {
     const uint32_t plane_bytes = (uint32_t)(HW * ELEM);
     const char* pvol = (const char*)a.pred + b * D * HW * ELEM;
     const char* tvol = (const char*)a.target + b * D * HW * ELEM;
+    char* const gvol = ADJ ? (char*)a.grad + b * D * HW * ELEM : nullptr;
 
     // ---- F: per-lane input columns
     uint32_t voff[J];
@@ -105,29 +107,51 @@ __global__ __launch_bounds__(NT, 1) void lncc_fused_kernel(FusedArgs a) {
             zaddr[j] = iy * G::ZS + ix;
         }
     }
-    // ---- per-lane items of the segment stages (at most one per stage)
-    const int yi = tid - G::Y_OFF;
-    const bool has_y = yi >= 0 && yi < G::YITEMS;
-    const int y_ax = has_y ? yi % G::AX : 0;
-    const int y_seg = has_y ? yi / G::AX : 0;
+    // P1 units: X (z-sums -> x-sums) then AX (adjoints -> x-sums); offsets into the source and
+    // destination buffers, the first output to store (segments shifted back repeat outputs), and
+    // the unit kind (0 none, 1 X, 2 AX)
+    int u_src[G::U1], u_dst[G::U1], u_fresh[G::U1], u_kind[G::U1];
+#pragma unroll
+    for (int k = 0; k < G::U1; ++k) {
+        const int u = tid + k * NT;
+        u_kind[k] = 0;
+        u_src[k] = 0;
+        u_dst[k] = 0;
+        u_fresh[k] = 0;
+        if (u < G::UX) {
+            const int q = u / G::XITEMS, it = u - q * G::XITEMS;
+            const int iy = it % G::IY, seg = it / G::IY;
+            const int start = min(seg * G::SX, G::AX - G::SX);
+            u_kind[k] = 1;
+            u_src[k] = q * G::ZP + iy * G::ZS + start;
+            u_dst[k] = q * G::XP + start * G::XS + iy;
+            u_fresh[k] = seg * G::SX - start;
+        } else if (ADJ && u < G::UX + G::UA) {
+            const int v = u - G::UX;
+            const int c = v / G::AITEMS, it = v - c * G::AITEMS;
+            const int ay = it % G::AY, start = (it / G::AY) * G::SA;
+            u_kind[k] = 2;
+            u_src[k] = c * G::GP + ay * G::GS + start;
+            u_dst[k] = c * G::GXP + start * G::GXS + ay;
+        }
+    }
+    // P0: Y items on lanes [0, YITEMS), AYs units on lanes [B_LANE0, NT)
+    const bool has_y = tid < G::YITEMS;
+    const int y_ax = has_y ? tid % G::AX : 0;
+    const int y_seg = has_y ? tid / G::AX : 0;
     const int y_start = min(y_seg * G::SY, G::AY - G::SY);
     const int y_fresh = y_seg * G::SY - y_start;
-    const int xi = tid - G::X_OFF;
-    const bool has_x = xi >= 0 && xi < G::XITEMS;
-    const int x_iy = has_x ? xi % G::IY : 0;
-    const int x_seg = has_x ? xi / G::IY : 0;
-    const int x_start = min(x_seg * G::SX, G::AX - G::SX);
-    const int x_fresh = x_seg * G::SX - x_start;
-    const int ai = tid - G::A_OFF;
-    const bool has_a = ADJ && ai >= 0 && ai < G::AITEMS;
-    const int a_ay = has_a ? ai % G::AY : 0;
-    const int a_start = has_a ? (ai / G::AY) * G::SA : 0;
-    const int bi = tid - G::B_OFF;
-    const bool has_b = ADJ && bi >= 0 && bi < G::BITEMS;
-    const int b_ox = has_b ? bi % TX : 0;
-    const int b_start = has_b ? (bi / TX) * G::SB : 0;
+    const bool has_b = ADJ && tid >= G::B_LANE0;
+    int b_src = 0, b_dst = 0;
+    if (has_b) {
+        const int v = tid - G::B_LANE0;
+        const int c = v / G::BITEMS, it = v - c * G::BITEMS;
+        const int ox = it % TX, start = (it / TX) * G::SB;
+        b_src = c * G::GXP + ox * G::GXS + start;
+        b_dst = c * G::GYP + start * G::GYS + ox;
+    }
     const bool has_z = ADJ && tid < G::NOUT;
-    const int z_ox = tid % TX, z_oy = tid / TX;
+    const int z_ox = tid % TX, z_oy = min(tid / TX, TY - 1);
     const bool z_in = has_z && x0 + z_ox < Wd && y0 + z_oy < Hd;
     const uint32_t z_voff = z_in ? (uint32_t)(((y0 + z_oy) * Wd + x0 + z_ox) * ELEM) : kOOB;
 
@@ -175,67 +199,6 @@ __global__ __launch_bounds__(NT, 1) void lncc_fused_kernel(FusedArgs a) {
 
             // ============================ phase P0 ============================
             float pzcur, tzcur;  // p,t at this step's output plane
-            // F(zi): z-sums of the input region
-            {
-                float pc[J], tc[J], po[J], to[J];
-#pragma unroll
-                for (int j = 0; j < J; ++j) {
-                    pc[j] = pnext[j];
-                    tc[j] = tnext[j];
-                    po[j] = pold[j];
-                    to[j] = told[j];
-                }
-                const float pzc = pz, tzc = tzz;
-                // prefetch plane zi+1, plane zi+1-k (leaving the window) and the output plane of step+1
-                const int zn = zi + 1, zq = zi + 1 - K, zon = zi - 1 - 2 * HH;
-                if (zn < zhi && zn < D) {
-                    const __amdgpu_buffer_rsrc_t rp = make_rsrc(pvol + (int64_t)zn * HW * ELEM, plane_bytes);
-                    const __amdgpu_buffer_rsrc_t rt = make_rsrc(tvol + (int64_t)zn * HW * ELEM, plane_bytes);
-#pragma unroll
-                    for (int j = 0; j < J; ++j) {
-                        pnext[j] = load_elem<BF16>(rp, voff[j]);
-                        tnext[j] = load_elem<BF16>(rt, voff[j]);
-                    }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < J; ++j) { pnext[j] = 0.f; tnext[j] = 0.f; }
-                }
-                if (zq >= zlo && zq < D && zn < zhi) {
-                    const __amdgpu_buffer_rsrc_t rp = make_rsrc(pvol + (int64_t)zq * HW * ELEM, plane_bytes);
-                    const __amdgpu_buffer_rsrc_t rt = make_rsrc(tvol + (int64_t)zq * HW * ELEM, plane_bytes);
-#pragma unroll
-                    for (int j = 0; j < J; ++j) {
-                        pold[j] = load_elem<BF16>(rp, voff[j]);
-                        told[j] = load_elem<BF16>(rt, voff[j]);
-                    }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < J; ++j) { pold[j] = 0.f; told[j] = 0.f; }
-                }
-                if constexpr (ADJ) {
-                    if (zon >= z0 && zon < z1) {
-                        const __amdgpu_buffer_rsrc_t rp = make_rsrc(pvol + (int64_t)zon * HW * ELEM, plane_bytes);
-                        const __amdgpu_buffer_rsrc_t rt = make_rsrc(tvol + (int64_t)zon * HW * ELEM, plane_bytes);
-                        pz = load_elem<BF16>(rp, z_voff);
-                        tzz = load_elem<BF16>(rt, z_voff);
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < J; ++j) {
-                    const float p = pc[j], t = tc[j];
-                    zsum[j][0] += p - po[j];
-                    zsum[j][1] += t - to[j];
-                    zsum[j][2] = fmaf(p, p, fmaf(-po[j], po[j], zsum[j][2]));
-                    zsum[j][3] = fmaf(t, t, fmaf(-to[j], to[j], zsum[j][3]));
-                    zsum[j][4] = fmaf(p, t, fmaf(-po[j], to[j], zsum[j][4]));
-                    if (zaddr[j] >= 0) {
-#pragma unroll
-                        for (int q = 0; q < 5; ++q) Zs[q * G::ZP + zaddr[j]] = zsum[j][q];
-                    }
-                }
-                pzcur = pzc;
-                tzcur = tzc;
-            }
             // Y(zi-1): box sums, ncc, adjoint coefficients at plane zcY
             const int zcY = zi - 1 - HH;
             const bool actY = zcY >= zc_lo && zcY < zc_hi;
@@ -289,48 +252,82 @@ __global__ __launch_bounds__(NT, 1) void lncc_fused_kernel(FusedArgs a) {
                 }
                 loss_acc += (double)lsum;
             }
-            // AYs(zi-2): y-sums of alpha, beta, gamma at plane zcB
+            // AYs(zi-2): y-sums of alpha, beta, gamma at plane zcB (one quantity per unit)
             const int zcB = zi - 2 - HH;
             const bool actB = ADJ && zcB >= zc_lo && zcB < zc_hi;
             if constexpr (ADJ) {
                 if (actB && has_b) {
+                    float o[G::SB];
+                    window_sums<HH, G::SB>(GXs + b_src, o);
 #pragma unroll
-                    for (int c = 0; c < 3; ++c) {
-                        float o[G::SB];
-                        window_sums<HH, G::SB>(GXs + c * G::GXP + b_ox * G::GXS + b_start, o);
+                    for (int i = 0; i < G::SB; ++i) GY[b_dst + i * G::GYS] = o[i];
+                }
+            }
+            // F(zi): z-sums of the input region. Consume the planes prefetched one step ago, then
+            // prefetch the next ones. Every global access of the loop is issued unconditionally
+            // (inactive ones through a zero-sized buffer), so the number of outstanding memory
+            // operations is the same on every path and the waits before use stay exact.
+            {
 #pragma unroll
-                        for (int i = 0; i < G::SB; ++i) GY[c * G::GYP + (b_start + i) * G::GYS + b_ox] = o[i];
+                for (int j = 0; j < J; ++j) {
+                    const float p = pnext[j], t = tnext[j], po = pold[j], to = told[j];
+                    zsum[j][0] += p - po;
+                    zsum[j][1] += t - to;
+                    zsum[j][2] = fmaf(p, p, fmaf(-po, po, zsum[j][2]));
+                    zsum[j][3] = fmaf(t, t, fmaf(-to, to, zsum[j][3]));
+                    zsum[j][4] = fmaf(p, t, fmaf(-po, to, zsum[j][4]));
+                    if (zaddr[j] >= 0) {
+#pragma unroll
+                        for (int q = 0; q < 5; ++q) Zs[q * G::ZP + zaddr[j]] = zsum[j][q];
                     }
+                }
+                pzcur = pz;
+                tzcur = tzz;
+                // prefetch plane zi+1, plane zi+1-k (leaving the window) and the next output plane
+                const int zn = zi + 1, zq = zi + 1 - K, zon = zi - 1 - 2 * HH;
+                const bool okn = zn < zhi && zn < D;
+                const bool okq = zq >= zlo && zq < D && zn < zhi;
+                const __amdgpu_buffer_rsrc_t rpn = plane_rsrc(pvol, zn, D, HW * ELEM, okn);
+                const __amdgpu_buffer_rsrc_t rtn = plane_rsrc(tvol, zn, D, HW * ELEM, okn);
+                const __amdgpu_buffer_rsrc_t rpq = plane_rsrc(pvol, zq, D, HW * ELEM, okq);
+                const __amdgpu_buffer_rsrc_t rtq = plane_rsrc(tvol, zq, D, HW * ELEM, okq);
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    pnext[j] = load_elem<BF16>(rpn, voff[j]);
+                    tnext[j] = load_elem<BF16>(rtn, voff[j]);
+                    pold[j] = load_elem<BF16>(rpq, voff[j]);
+                    told[j] = load_elem<BF16>(rtq, voff[j]);
+                }
+                if constexpr (ADJ) {
+                    const bool oko = zon >= z0 && zon < z1;
+                    pz = load_elem<BF16>(plane_rsrc(pvol, zon, D, HW * ELEM, oko), z_voff);
+                    tzz = load_elem<BF16>(plane_rsrc(tvol, zon, D, HW * ELEM, oko), z_voff);
                 }
             }
             __syncthreads();
 
             // ============================ phase P1 ============================
-            // X(zi): x-sums of the z-sums (feeds Y at the next plane)
+            // X(zi) and AX(zi-1): x-sums of the z-sums (feeds Y at the next plane) and of alpha,
+            // beta, gamma at plane zcY, one quantity of one segment per unit
             const int zcX = zi - HH;
-            if (zcX >= zc_lo && zcX < zc_hi && has_x) {
+            const bool actX = zcX >= zc_lo && zcX < zc_hi;
 #pragma unroll
-                for (int q = 0; q < 5; ++q) {
+            for (int k = 0; k < G::U1; ++k) {
+                const bool run = (u_kind[k] == 1 && actX) || (u_kind[k] == 2 && actY);
+                if (run) {
+                    const float* src = (u_kind[k] == 1 ? Zs : Gs) + u_src[k];
+                    float* dst = (u_kind[k] == 1 ? Xs : GXs) + u_dst[k];
                     float o[G::SX];
-                    window_sums<HH, G::SX>(Zs + q * G::ZP + x_iy * G::ZS + x_start, o);
+                    window_sums<HH, G::SX>(src, o);
 #pragma unroll
                     for (int i = 0; i < G::SX; ++i)
-                        if (i >= x_fresh) Xs[q * G::XP + (x_start + i) * G::XS + x_iy] = o[i];
+                        if (i >= u_fresh[k]) dst[i * G::XS] = o[i];
                 }
             }
             if constexpr (ADJ) {
-                // AX(zi-1): x-sums of alpha, beta, gamma at plane zcY
-                if (actY && has_a) {
-#pragma unroll
-                    for (int c = 0; c < 3; ++c) {
-                        float o[G::SA];
-                        window_sums<HH, G::SA>(Gs + c * G::GP + a_ay * G::GS + a_start, o);
-#pragma unroll
-                        for (int i = 0; i < G::SA; ++i) GXs[c * G::GXP + (a_start + i) * G::GXS + a_ay] = o[i];
-                    }
-                }
-                // AZ(zi-2): z ring of the xy-sums, combine at the output plane zo
-                if (has_z) {
+                // AZ(zi-2): z ring of the xy-sums, combine at the output plane zo (lanes without an
+                // output column run on a clamped one and store out of range, i.e. nothing)
+                {
                     float ys[3];
 #pragma unroll
                     for (int c = 0; c < 3; ++c) ys[c] = actB ? GY[c * G::GYP + z_oy * G::GYS + z_ox] : 0.f;
@@ -340,18 +337,15 @@ __global__ __launch_bounds__(NT, 1) void lncc_fused_kernel(FusedArgs a) {
                         gring[c][r] = ys[c];
                     }
                     const int zo = zcB - HH;
-                    const int gx = x0 + z_ox, gy = y0 + z_oy;
-                    if (zo >= z0 && zo < z1 && gx < Wd && gy < Hd) {
-                        const float g = a.gscale * fmaf(inv_n, gz[0], fmaf(pzcur, gz[1], -tzcur * gz[2]));
-                        store_elem<BF16>(a.grad, ((b * D + zo) * Hd + gy) * (int64_t)Wd + gx, g);
-                    }
+                    const float g = a.gscale * fmaf(inv_n, gz[0], fmaf(pzcur, gz[1], -tzcur * gz[2]));
+                    store_elem_buf<BF16>(plane_rsrc(gvol, zo, D, HW * ELEM, zo >= z0 && zo < z1), z_voff, g);
                 }
             }
             __syncthreads();
         });
     }
 
-    // ---- workgroup partial of the ncc sum: wave64 reduction, then the 16 waves in fixed order
+    // ---- workgroup partial of the ncc sum: wave64 reduction, then the waves in fixed order
     if constexpr (MODE == MODE_MAPS) return;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) loss_acc += __shfl_xor(loss_acc, off, 64);
