@@ -86,7 +86,7 @@ def main():
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested). The loss is "
               "independent per (N,C) volume; multi-GPU use is data-parallel with no collective in "
-              "the loss, see DESIGN.md.", file=sys.stderr)
+              "the loss.", file=sys.stderr)
         sys.exit(2)
     import torch
 

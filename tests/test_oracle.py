@@ -193,3 +193,15 @@ def test_round_bf16_matches_torch():
     ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     assert np.array_equal(ours, ref)
     assert np.isnan(O.round_bf16(np.array([np.nan], np.float32))[0])
+
+
+@pytest.mark.parametrize("name", ["cpu_k3", "nc_k5", "dr1_k3", "edge_k7_1x3x7x9x11"])
+def test_torch_port_matches_golden(name):
+    """The CPU baseline (the reference's naive torch path, restated) reproduces the golden vectors."""
+    import torch_lncc_port
+    d = np.load(os.path.join(GOLDEN, name + ".npz"))
+    loss, g = torch_lncc_port.loss_and_grad(torch.from_numpy(d["pred"]), torch.from_numpy(d["target"]),
+                                            int(d["k"]), float(d["smooth_dr"]))
+    assert abs(float(loss) - float(d["loss"])) <= 1e-6 * max(abs(float(d["loss"])), 1e-3)
+    cos, rel = _cos_rel(g.numpy(), d["grad"])
+    assert cos > 0.999999 and rel < 1e-5
