@@ -114,19 +114,19 @@ struct Geo {
     static constexpr int J = cdiv(NIN, NT);               // input columns per lane
     static constexpr int NOUT = TX * TY;                  // output columns (one lane each)
     // X: x-sums of the five z-sums; items (iy, seg) over rows iy < IY, outputs ax < AX
-    static constexpr int SX = 8, XSEG = cdiv(AX, SX), XITEMS = IY * XSEG;
+    static constexpr int SX = cdiv(AX, 4) * 2, XSEG = cdiv(AX, SX), XITEMS = IY * XSEG;
     // Y: y-sums -> box sums, ncc, adjoints; items (ax, seg), outputs ay < AY
-    static constexpr int SY = 2, YSEG = cdiv(AY, SY), YITEMS = AX * YSEG;
+    static constexpr int SY = 4, YSEG = cdiv(AY, SY), YITEMS = AX * YSEG;
     // AX: x-sums of alpha, beta, gamma; items (ay, seg), outputs ox < TX
-    static constexpr int SA = 8, ASEG = TX / SA, AITEMS = AY * ASEG;
+    static constexpr int SA = 16, ASEG = TX / SA, AITEMS = AY * ASEG;
     // AYs: y-sums of the three; items (ox, seg), outputs oy < TY
-    static constexpr int SB = 8, BSEG = TY / SB, BITEMS = TX * BSEG;
+    static constexpr int SB = TY / 2, BSEG = TY / SB, BITEMS = TX * BSEG;
     // Work units of the running-sum passes are single quantities of one segment, spread over all
     // lanes: phase P1 runs the X units (5 per item) then the AX units (3 per item); phase P0 runs
     // Y items on the first lanes and the AYs units (3 per item) on the last lanes.
     static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, U1 = cdiv(UX + UA, NT);
     static constexpr int UB = 3 * BITEMS, B_LANE0 = NT - UB;
-    static_assert(YITEMS <= NT && UB <= NT && SX == SA, "lanes");
+    static_assert(YITEMS <= NT && UB <= NT && SX % 2 == 0 && SY % 2 == 0, "lanes");
     static_assert(AX >= SX && AY >= SY && TX % SA == 0 && TY % SB == 0, "segments");
     // LDS layout (floats): Zs[5][IY][ZS], XsT[5][AX][XS] (transposed), Gs[3][AY][GS],
     // GXsT[3][TX][GXS] (transposed), GY[3][TY][GYS]

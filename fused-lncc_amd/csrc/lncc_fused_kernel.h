@@ -35,16 +35,20 @@
 
 namespace fl {
 
-// Running window sums of width 2H+1 over S consecutive outputs from S+2H inputs read as float2.
-template <int H, int S>
-__device__ __forceinline__ void window_sums(const float* __restrict__ src, float (&out)[S]) {
-    float v[S + 2 * H];
+// Loads NV consecutive floats from an 8-byte aligned LDS address as float2s.
+template <int NV>
+__device__ __forceinline__ void lds_row(const float* __restrict__ src, float (&v)[NV]) {
 #pragma unroll
-    for (int m = 0; m < (S + 2 * H) / 2; ++m) {
+    for (int m = 0; m < NV / 2; ++m) {
         const float2 f = reinterpret_cast<const float2*>(src)[m];
         v[2 * m] = f.x;
         v[2 * m + 1] = f.y;
     }
+}
+
+// Running window sums of width 2H+1: out[i] = v[i] + ... + v[i+2H] for i < S.
+template <int H, int S>
+__device__ __forceinline__ void window_sums(const float (&v)[S + 2 * H], float (&out)[S]) {
     float acc = v[0];
 #pragma unroll
     for (int i = 1; i <= 2 * H; ++i) acc += v[i];
@@ -203,9 +207,12 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             const int zcY = zi - 1 - HH;
             const bool actY = zcY >= zc_lo && zcY < zc_hi;
             if (actY && has_y) {
-                float S[5][G::SY];
+                // all five rows are read before any arithmetic, so their LDS latencies overlap
+                float yv[5][G::SY + 2 * HH], S[5][G::SY];
 #pragma unroll
-                for (int q = 0; q < 5; ++q) window_sums<HH, G::SY>(Xs + q * G::XP + y_ax * G::XS + y_start, S[q]);
+                for (int q = 0; q < 5; ++q) lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv[q]);
+#pragma unroll
+                for (int q = 0; q < 5; ++q) window_sums<HH, G::SY>(yv[q], S[q]);
                 const int gx = x0 - HH + y_ax;
                 const bool inx = gx >= 0 && gx < Wd;
                 const bool corex = y_ax >= HH && y_ax < HH + TX;
@@ -230,12 +237,14 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     const bool core = corex && ay >= HH && ay < HH + TY;
                     if (count && inv && core && fresh) lsum += nccc;
                     if constexpr (ADJ) {
-                        const float uu = cr * vt;
+                        // masking cr masks all three coefficients (alpha, beta, gamma are multiples of it)
+                        const float crm = live ? cr : 0.f;
+                        const float uu = crm * vt;
                         const float w = fmaf(-Sp, uu, St);
                         if (fresh) {
-                            Gs[0 * G::GP + ay * G::GS + y_ax] = live ? cr * w : 0.f;
-                            Gs[1 * G::GP + ay * G::GS + y_ax] = live ? cr * uu : 0.f;
-                            Gs[2 * G::GP + ay * G::GS + y_ax] = live ? cr : 0.f;
+                            Gs[0 * G::GP + ay * G::GS + y_ax] = crm * w;
+                            Gs[1 * G::GP + ay * G::GS + y_ax] = crm * uu;
+                            Gs[2 * G::GP + ay * G::GS + y_ax] = crm;
                         }
                     }
                     if constexpr (MODE == MODE_MAPS) {
@@ -257,8 +266,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             const bool actB = ADJ && zcB >= zc_lo && zcB < zc_hi;
             if constexpr (ADJ) {
                 if (actB && has_b) {
-                    float o[G::SB];
-                    window_sums<HH, G::SB>(GXs + b_src, o);
+                    float v[G::SB + 2 * HH], o[G::SB];
+                    lds_row(GXs + b_src, v);
+                    window_sums<HH, G::SB>(v, o);
 #pragma unroll
                     for (int i = 0; i < G::SB; ++i) GY[b_dst + i * G::GYS] = o[i];
                 }
@@ -313,15 +323,19 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             const bool actX = zcX >= zc_lo && zcX < zc_hi;
 #pragma unroll
             for (int k = 0; k < G::U1; ++k) {
-                const bool run = (u_kind[k] == 1 && actX) || (u_kind[k] == 2 && actY);
-                if (run) {
-                    const float* src = (u_kind[k] == 1 ? Zs : Gs) + u_src[k];
-                    float* dst = (u_kind[k] == 1 ? Xs : GXs) + u_dst[k];
-                    float o[G::SX];
-                    window_sums<HH, G::SX>(src, o);
+                if (u_kind[k] == 1 && actX) {
+                    float v[G::SX + 2 * HH], o[G::SX];
+                    lds_row(Zs + u_src[k], v);
+                    window_sums<HH, G::SX>(v, o);
 #pragma unroll
                     for (int i = 0; i < G::SX; ++i)
-                        if (i >= u_fresh[k]) dst[i * G::XS] = o[i];
+                        if (i >= u_fresh[k]) Xs[u_dst[k] + i * G::XS] = o[i];
+                } else if (ADJ && u_kind[k] == 2 && actY) {
+                    float v[G::SA + 2 * HH], o[G::SA];
+                    lds_row(Gs + u_src[k], v);
+                    window_sums<HH, G::SA>(v, o);
+#pragma unroll
+                    for (int i = 0; i < G::SA; ++i) GXs[u_dst[k] + i * G::XS] = o[i];
                 }
             }
             if constexpr (ADJ) {
