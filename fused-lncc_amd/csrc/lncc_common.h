@@ -25,11 +25,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 
 // Resource for plane z (clamped into [0, D)) of a volume; `valid == false` gives a zero-sized
-// buffer, so loads through it return 0 and stores through it are dropped.
+// buffer, so loads through it return 0 and stores through it are dropped. z and valid must be
+// workgroup-uniform; the explicit readfirstlane keeps the address arithmetic on the scalar unit
+// (a clamp that the compiler selects as a VALU op would otherwise force a per-lane loop around
+// every access through the resource).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void* vol, int z, int D, int64_t plane_bytes,
                                                                bool valid) {
-    const int zc = z < 0 ? 0 : (z >= D ? D - 1 : z);
-    return make_rsrc((const char*)vol + (int64_t)zc * plane_bytes, valid ? (uint32_t)plane_bytes : 0u);
+    const int zc = __builtin_amdgcn_readfirstlane(z < 0 ? 0 : (z >= D ? D - 1 : z));
+    const int nb = __builtin_amdgcn_readfirstlane(valid ? (int)plane_bytes : 0);
+    return make_rsrc((const char*)vol + (int64_t)zc * plane_bytes, (uint32_t)nb);
 }
 
 template <bool BF16>
@@ -101,9 +105,10 @@ constexpr int rup64(int n) { return (n + 63) / 64 * 64; }
 //   input region   ix in [0,IX), iy in [0,IY)  <-> global (x0-2H+ix, y0-2H+iy)
 //   adjoint region ax in [0,AX), ay in [0,AY)  <-> global (x0-H+ax,  y0-H+ay)
 //   output tile    ox in [0,TX), oy in [0,TY)  <-> global (x0+ox,    y0+oy)
-// Running-sum passes work on segments of S consecutive outputs; a segment that would overrun the
-// range is shifted back to end at the range's end (its first outputs then repeat the previous
-// segment's and are neither stored twice nor counted twice).
+// Running-sum passes work on segments of S consecutive outputs. The X and Y passes round their
+// output range up to whole segments: the extra outputs read row padding and land in padding rows
+// of the destination that no later pass reads (and that the loss never counts), so no lane needs
+// a per-output store mask.
 template <int H>
 struct Geo {
     static constexpr int K = 2 * H + 1;
@@ -113,10 +118,10 @@ struct Geo {
     static constexpr int NIN = IX * IY;
     static constexpr int J = cdiv(NIN, NT);               // input columns per lane
     static constexpr int NOUT = TX * TY;                  // output columns (one lane each)
-    // X: x-sums of the five z-sums; items (iy, seg) over rows iy < IY, outputs ax < AX
-    static constexpr int SX = cdiv(AX, 4) * 2, XSEG = cdiv(AX, SX), XITEMS = IY * XSEG;
-    // Y: y-sums -> box sums, ncc, adjoints; items (ax, seg), outputs ay < AY
-    static constexpr int SY = 4, YSEG = cdiv(AY, SY), YITEMS = AX * YSEG;
+    // X: x-sums of the five z-sums; items (iy, seg) over rows iy < IY, outputs ax < XR (>= AX)
+    static constexpr int SX = cdiv(AX, 4) * 2, XSEG = 2, XR = XSEG * SX, XITEMS = IY * XSEG;
+    // Y: y-sums -> box sums, ncc, adjoints; items (ax, seg), outputs ay < YR (>= AY)
+    static constexpr int SY = 4, YSEG = cdiv(AY, SY), YR = YSEG * SY, YITEMS = AX * YSEG;
     // AX: x-sums of alpha, beta, gamma; items (ay, seg), outputs ox < TX
     static constexpr int SA = 16, ASEG = TX / SA, AITEMS = AY * ASEG;
     // AYs: y-sums of the three; items (ox, seg), outputs oy < TY
@@ -127,13 +132,14 @@ struct Geo {
     static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, U1 = cdiv(UX + UA, NT);
     static constexpr int UB = 3 * BITEMS, B_LANE0 = NT - UB;
     static_assert(YITEMS <= NT && UB <= NT && SX % 2 == 0 && SY % 2 == 0, "lanes");
-    static_assert(AX >= SX && AY >= SY && TX % SA == 0 && TY % SB == 0, "segments");
-    // LDS layout (floats): Zs[5][IY][ZS], XsT[5][AX][XS] (transposed), Gs[3][AY][GS],
+    static_assert(XR >= AX && TX % SA == 0 && TY % SB == 0, "segments");
+    // LDS layout (floats): Zs[5][IY][ZS], XsT[5][XR][XS] (transposed), Gs[3][YR][GS],
     // GXsT[3][TX][GXS] (transposed), GY[3][TY][GYS]
-    // XS == GXS: the X and AX passes share one code path (same destination stride)
     static constexpr int ZS = stride2(IX), XS = stride2(cmax(IY, AY)), GS = stride2(AX), GXS = XS;
     static constexpr int GYS = TX + 1;
-    static constexpr int ZP = IY * ZS, XP = AX * XS, GP = AY * GS, GXP = TX * GXS, GYP = TY * GYS;
+    // the rounded-up segments read at most this far into a row (padding, never out of the array)
+    static_assert(XR + 2 * H <= ZS && YR + 2 * H <= XS, "row padding");
+    static constexpr int ZP = IY * ZS, XP = XR * XS, GP = YR * GS, GXP = TX * GXS, GYP = TY * GYS;
     static constexpr int Z_OFF = 0, XS_OFF = 5 * ZP, G_OFF = XS_OFF + 5 * XP, GX_OFF = G_OFF + 3 * GP;
     static constexpr int GY_OFF = GX_OFF + 3 * GXP;
     static constexpr int LDS_FLOATS = GY_OFF + 3 * GYP;

@@ -112,24 +112,21 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
         }
     }
     // P1 units: X (z-sums -> x-sums) then AX (adjoints -> x-sums); offsets into the source and
-    // destination buffers, the first output to store (segments shifted back repeat outputs), and
-    // the unit kind (0 none, 1 X, 2 AX)
-    int u_src[G::U1], u_dst[G::U1], u_fresh[G::U1], u_kind[G::U1];
+    // destination buffers and the unit kind (0 none, 1 X, 2 AX)
+    int u_src[G::U1], u_dst[G::U1], u_kind[G::U1];
 #pragma unroll
     for (int k = 0; k < G::U1; ++k) {
         const int u = tid + k * NT;
         u_kind[k] = 0;
         u_src[k] = 0;
         u_dst[k] = 0;
-        u_fresh[k] = 0;
         if (u < G::UX) {
             const int q = u / G::XITEMS, it = u - q * G::XITEMS;
             const int iy = it % G::IY, seg = it / G::IY;
-            const int start = min(seg * G::SX, G::AX - G::SX);
+            const int start = seg * G::SX;
             u_kind[k] = 1;
             u_src[k] = q * G::ZP + iy * G::ZS + start;
             u_dst[k] = q * G::XP + start * G::XS + iy;
-            u_fresh[k] = seg * G::SX - start;
         } else if (ADJ && u < G::UX + G::UA) {
             const int v = u - G::UX;
             const int c = v / G::AITEMS, it = v - c * G::AITEMS;
@@ -143,8 +140,21 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const bool has_y = tid < G::YITEMS;
     const int y_ax = has_y ? tid % G::AX : 0;
     const int y_seg = has_y ? tid / G::AX : 0;
-    const int y_start = min(y_seg * G::SY, G::AY - G::SY);
-    const int y_fresh = y_seg * G::SY - y_start;
+    const int y_start = y_seg * G::SY;
+    // per output of the Y segment: inside the volume (ncc and adjoints live) / counted in the loss
+    // (inside the volume and in the output tile); the same on every plane
+    bool y_inv[G::SY], y_core[G::SY];
+    {
+        const int gx = x0 - HH + y_ax;
+        const bool inx = has_y && gx >= 0 && gx < Wd;
+        const bool corex = y_ax >= HH && y_ax < HH + TX;
+#pragma unroll
+        for (int i = 0; i < G::SY; ++i) {
+            const int ay = y_start + i, gy = y0 - HH + ay;
+            y_inv[i] = inx && gy >= 0 && gy < Hd;
+            y_core[i] = y_inv[i] && corex && ay >= HH && ay < HH + TY;
+        }
+    }
     const bool has_b = ADJ && tid >= G::B_LANE0;
     int b_src = 0, b_dst = 0;
     if (has_b) {
@@ -213,15 +223,11 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 for (int q = 0; q < 5; ++q) lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv[q]);
 #pragma unroll
                 for (int q = 0; q < 5; ++q) window_sums<HH, G::SY>(yv[q], S[q]);
-                const int gx = x0 - HH + y_ax;
-                const bool inx = gx >= 0 && gx < Wd;
-                const bool corex = y_ax >= HH && y_ax < HH + TX;
                 const bool count = zcY >= z0 && zcY < z1;
                 float lsum = 0.f;
 #pragma unroll
                 for (int i = 0; i < G::SY; ++i) {
                     const int ay = y_start + i;
-                    const bool fresh = i >= y_fresh;
                     const float Sp = S[0][i], St = S[1][i], Spp = S[2][i], Stt = S[3][i], Spt = S[4][i];
                     const float mp = Sp * inv_n, mt = St * inv_n;
                     const float cross = fmaf(-mp, St, Spt);
@@ -230,27 +236,23 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     const float rr = __builtin_amdgcn_rcpf(vp * vt);
                     const float cr = cross * rr;
                     const float ncc = cross * cr;
-                    const int gy = y0 - HH + ay;
-                    const bool inv = inx && gy >= 0 && gy < Hd;
-                    const bool live = inv && (ncc < 1.0f);
+                    const bool live = y_inv[i] && (ncc < 1.0f);
                     const float nccc = (ncc >= 1.0f) ? 1.0f : ncc;
-                    const bool core = corex && ay >= HH && ay < HH + TY;
-                    if (count && inv && core && fresh) lsum += nccc;
+                    if (count && y_core[i]) lsum += nccc;
                     if constexpr (ADJ) {
                         // masking cr masks all three coefficients (alpha, beta, gamma are multiples of it)
                         const float crm = live ? cr : 0.f;
                         const float uu = crm * vt;
                         const float w = fmaf(-Sp, uu, St);
-                        if (fresh) {
-                            Gs[0 * G::GP + ay * G::GS + y_ax] = crm * w;
-                            Gs[1 * G::GP + ay * G::GS + y_ax] = crm * uu;
-                            Gs[2 * G::GP + ay * G::GS + y_ax] = crm;
-                        }
+                        Gs[0 * G::GP + ay * G::GS + y_ax] = crm * w;
+                        Gs[1 * G::GP + ay * G::GS + y_ax] = crm * uu;
+                        Gs[2 * G::GP + ay * G::GS + y_ax] = crm;
                     }
                     if constexpr (MODE == MODE_MAPS) {
-                        if (count && inv && core && fresh) {
+                        if (count && y_core[i]) {
                             const float uu = cr * vt;
                             const float w = fmaf(-Sp, uu, St);
+                            const int gx = x0 - HH + y_ax, gy = y0 - HH + ay;
                             const int64_t o = ((b * D + zcY) * Hd + gy) * (int64_t)Wd + gx;
                             a.ncc_map[o] = nccc;
                             a.a_map[o] = live ? -2.f * inv_n * (cr * w) : 0.f;
@@ -328,8 +330,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     lds_row(Zs + u_src[k], v);
                     window_sums<HH, G::SX>(v, o);
 #pragma unroll
-                    for (int i = 0; i < G::SX; ++i)
-                        if (i >= u_fresh[k]) Xs[u_dst[k] + i * G::XS] = o[i];
+                    for (int i = 0; i < G::SX; ++i) Xs[u_dst[k] + i * G::XS] = o[i];
                 } else if (ADJ && u_kind[k] == 2 && actY) {
                     float v[G::SA + 2 * HH], o[G::SA];
                     lds_row(Gs + u_src[k], v);
