@@ -177,7 +177,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 
     // F state: running z-sums; p,t of the next plane and of the plane leaving the window (prefetched)
     float zsum[J][5], pnext[J], tnext[J], pold[J], told[J];
-    float pz = 0.f, tzz = 0.f;  // AZ: p,t at the next step's output plane (prefetched)
+    float pz = 0.f, tzz = 0.f;  // AZ: p,t at this step's output plane (prefetched one step ahead)
 #pragma unroll
     for (int j = 0; j < J; ++j) {
 #pragma unroll
@@ -212,7 +212,6 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             if (zi >= zhi) return;
 
             // ============================ phase P0 ============================
-            float pzcur, tzcur;  // p,t at this step's output plane
             // Y(zi-1): box sums, ncc, adjoint coefficients at plane zcY
             const int zcY = zi - 1 - HH;
             const bool actY = zcY >= zc_lo && zcY < zc_hi;
@@ -293,10 +292,8 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                         for (int q = 0; q < 5; ++q) Zs[q * G::ZP + zaddr[j]] = zsum[j][q];
                     }
                 }
-                pzcur = pz;
-                tzcur = tzz;
-                // prefetch plane zi+1, plane zi+1-k (leaving the window) and the next output plane
-                const int zn = zi + 1, zq = zi + 1 - K, zon = zi - 1 - 2 * HH;
+                // prefetch plane zi+1 and plane zi+1-k (leaving the window)
+                const int zn = zi + 1, zq = zi + 1 - K;
                 const bool okn = zn < zhi && zn < D;
                 const bool okq = zq >= zlo && zq < D && zn < zhi;
                 const __amdgpu_buffer_rsrc_t rpn = plane_rsrc(pvol, zn, D, HW * ELEM, okn);
@@ -309,11 +306,6 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     tnext[j] = load_elem<BF16>(rtn, voff[j]);
                     pold[j] = load_elem<BF16>(rpq, voff[j]);
                     told[j] = load_elem<BF16>(rtq, voff[j]);
-                }
-                if constexpr (ADJ) {
-                    const bool oko = zon >= z0 && zon < z1;
-                    pz = load_elem<BF16>(plane_rsrc(pvol, zon, D, HW * ELEM, oko), z_voff);
-                    tzz = load_elem<BF16>(plane_rsrc(tvol, zon, D, HW * ELEM, oko), z_voff);
                 }
             }
             __syncthreads();
@@ -352,8 +344,14 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                         gring[c][r] = ys[c];
                     }
                     const int zo = zcB - HH;
-                    const float g = a.gscale * fmaf(inv_n, gz[0], fmaf(pzcur, gz[1], -tzcur * gz[2]));
+                    const float g = a.gscale * fmaf(inv_n, gz[0], fmaf(pz, gz[1], -tzz * gz[2]));
                     store_elem_buf<BF16>(plane_rsrc(gvol, zo, D, HW * ELEM, zo >= z0 && zo < z1), z_voff, g);
+                    // prefetch p,t at the next step's output plane; issued after this step's use, so
+                    // one register each suffices and no copy has to wait for the load
+                    const int zon = zo + 1;
+                    const bool oko = zon >= z0 && zon < z1;
+                    pz = load_elem<BF16>(plane_rsrc(pvol, zon, D, HW * ELEM, oko), z_voff);
+                    tzz = load_elem<BF16>(plane_rsrc(tvol, zon, D, HW * ELEM, oko), z_voff);
                 }
             }
             __syncthreads();
