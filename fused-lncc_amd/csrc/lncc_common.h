@@ -36,6 +36,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const void* vol, in
     return make_rsrc((const char*)vol + (int64_t)zc * plane_bytes, (uint32_t)nb);
 }
 
+// Resource for `bytes` bytes at a workgroup-uniform address; `valid == false` gives a zero-sized
+// buffer (the address is then never dereferenced).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_at(uint64_t addr, uint32_t bytes, bool valid) {
+    return make_rsrc((const void*)(uintptr_t)addr, valid ? bytes : 0u);
+}
+
 template <bool BF16>
 __device__ __forceinline__ float load_elem(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
     if constexpr (BF16) {

@@ -205,6 +205,17 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     double loss_acc = 0.0;
     const float inv_n = a.inv_n, dr = a.dr;
 
+    // Plane addresses advance by one plane per step: zoff = zi * plane size, and every plane the
+    // loop touches sits at a fixed plane distance from zi. A plane outside its valid range gets a
+    // zero-sized resource (its address is never dereferenced).
+    const uint64_t PB = (uint64_t)HW * ELEM;
+    const uint64_t pva = (uint64_t)(uintptr_t)pvol, tva = (uint64_t)(uintptr_t)tvol;
+    const uint64_t gva = (uint64_t)(uintptr_t)gvol;
+    uint64_t zoff = (uint64_t)zlo * PB;
+    const int zn_hi = min(zhi, D);                 // F: new plane zi+1 valid while zi+1 < zn_hi
+    const int zq_lo = zlo + K - 1, zq_hi = min(D + K - 1, zhi - 1);  // old plane zi+1-K: zi in [zq_lo, zq_hi)
+    constexpr int ZO = 2 + 2 * HH;                 // AZ: output plane zi-ZO
+
     for (int base = zlo; base < zhi; base += K) {
         static_for<0, K>([&](auto rc) __attribute__((always_inline)) {
             constexpr int r = decltype(rc)::value;
@@ -293,13 +304,11 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     }
                 }
                 // prefetch plane zi+1 and plane zi+1-k (leaving the window)
-                const int zn = zi + 1, zq = zi + 1 - K;
-                const bool okn = zn < zhi && zn < D;
-                const bool okq = zq >= zlo && zq < D && zn < zhi;
-                const __amdgpu_buffer_rsrc_t rpn = plane_rsrc(pvol, zn, D, HW * ELEM, okn);
-                const __amdgpu_buffer_rsrc_t rtn = plane_rsrc(tvol, zn, D, HW * ELEM, okn);
-                const __amdgpu_buffer_rsrc_t rpq = plane_rsrc(pvol, zq, D, HW * ELEM, okq);
-                const __amdgpu_buffer_rsrc_t rtq = plane_rsrc(tvol, zq, D, HW * ELEM, okq);
+                const bool okn = zi + 1 < zn_hi, okq = zi >= zq_lo && zi < zq_hi;
+                const __amdgpu_buffer_rsrc_t rpn = rsrc_at(pva + zoff + PB, plane_bytes, okn);
+                const __amdgpu_buffer_rsrc_t rtn = rsrc_at(tva + zoff + PB, plane_bytes, okn);
+                const __amdgpu_buffer_rsrc_t rpq = rsrc_at(pva + zoff - (K - 1) * PB, plane_bytes, okq);
+                const __amdgpu_buffer_rsrc_t rtq = rsrc_at(tva + zoff - (K - 1) * PB, plane_bytes, okq);
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
                     pnext[j] = load_elem<BF16>(rpn, voff[j]);
@@ -343,17 +352,17 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                         gz[c] += ys[c] - gring[c][r];
                         gring[c][r] = ys[c];
                     }
-                    const int zo = zcB - HH;
+                    const int zo = zi - ZO;
                     const float g = a.gscale * fmaf(inv_n, gz[0], fmaf(pz, gz[1], -tzz * gz[2]));
-                    store_elem_buf<BF16>(plane_rsrc(gvol, zo, D, HW * ELEM, zo >= z0 && zo < z1), z_voff, g);
+                    store_elem_buf<BF16>(rsrc_at(gva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, g);
                     // prefetch p,t at the next step's output plane; issued after this step's use, so
                     // one register each suffices and no copy has to wait for the load
-                    const int zon = zo + 1;
-                    const bool oko = zon >= z0 && zon < z1;
-                    pz = load_elem<BF16>(plane_rsrc(pvol, zon, D, HW * ELEM, oko), z_voff);
-                    tzz = load_elem<BF16>(plane_rsrc(tvol, zon, D, HW * ELEM, oko), z_voff);
+                    const bool oko = zo + 1 >= z0 && zo + 1 < z1;
+                    pz = load_elem<BF16>(rsrc_at(pva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
+                    tzz = load_elem<BF16>(rsrc_at(tva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
                 }
             }
+            zoff += PB;
             __syncthreads();
         });
     }
