@@ -102,9 +102,10 @@ constexpr int cmax(int a, int b) { return a > b ? a : b; }
 constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 constexpr int odd(int a) { return a | 1; }
 
-// Row stride (floats) for LDS rows read as float2 by lanes that step from row to row: even, and
-// = 2 mod 4 so that the 16 lanes served per cycle by a 64-bit read land on distinct bank pairs.
-constexpr int stride2(int n) { return (n % 4 == 2) ? n : (n % 4 == 3 ? n + 3 : (n % 4 == 0 ? n + 2 : n + 1)); }
+// Row stride (floats) for LDS rows read as float4 by lanes that step from row to row: = 4 mod 8,
+// so that the 8 lanes served per cycle by a 128-bit read land on distinct groups of 4 banks.
+constexpr int stride4(int n) { return n + ((12 - n % 8) % 8); }
+constexpr int rup4(int n) { return (n + 3) / 4 * 4; }
 constexpr int rup64(int n) { return (n + 63) / 64 * 64; }
 
 // Tile geometry for halo H (k = 2H+1). Coordinates inside a workgroup:
@@ -125,7 +126,7 @@ struct Geo {
     static constexpr int J = cdiv(NIN, NT);               // input columns per lane
     static constexpr int NOUT = TX * TY;                  // output columns (one lane each)
     // X: x-sums of the five z-sums; items (iy, seg) over rows iy < IY, outputs ax < XR (>= AX)
-    static constexpr int SX = cdiv(AX, 4) * 2, XSEG = 2, XR = XSEG * SX, XITEMS = IY * XSEG;
+    static constexpr int SX = rup4(cdiv(AX, 2)), XSEG = 2, XR = XSEG * SX, XITEMS = IY * XSEG;
     // Y: y-sums -> box sums, ncc, adjoints; items (ax, seg), outputs ay < YR (>= AY)
     static constexpr int SY = 4, YSEG = cdiv(AY, SY), YR = YSEG * SY, YITEMS = AX * YSEG;
     // AX: x-sums of alpha, beta, gamma; items (ay, seg), outputs ox < TX
@@ -137,19 +138,21 @@ struct Geo {
     // Y items on the first lanes and the AYs units (3 per item) on the last lanes.
     static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, U1 = cdiv(UX + UA, NT);
     static constexpr int UB = 3 * BITEMS, B_LANE0 = NT - UB;
-    static_assert(YITEMS <= NT && UB <= NT && SX % 2 == 0 && SY % 2 == 0, "lanes");
-    static_assert(XR >= AX && TX % SA == 0 && TY % SB == 0, "segments");
+    static_assert(YITEMS <= NT && UB <= NT, "lanes");
+    // every segment starts on a 16-byte boundary (rows are read as float4)
+    static_assert(XR >= AX && TX % SA == 0 && TY % SB == 0 && SX % 4 == 0 && SY % 4 == 0 &&
+                      SA % 4 == 0 && SB % 4 == 0, "segments");
     // LDS layout (floats): Zs[5][IY][ZS], XsT[5][XR][XS] (transposed), Gs[3][YR][GS],
-    // GXsT[3][TX][GXS] (transposed), GY[3][TY][GYS]
-    static constexpr int ZS = stride2(IX), XS = stride2(cmax(IY, AY)), GS = stride2(AX), GXS = XS;
-    static constexpr int GYS = TX + 1;
-    // the rounded-up segments read at most this far into a row (padding, never out of the array)
-    static_assert(XR + 2 * H <= ZS && YR + 2 * H <= XS, "row padding");
+    // GXsT[3][TX][GXS] (transposed), GY[3][TY][GYS]; each buffer but GY ends in PAD spare floats
+    static constexpr int ZS = stride4(IX), XS = stride4(cmax(IY, AY)), GS = stride4(AX), GXS = XS;
+    static constexpr int GYS = TX + 1, PAD = 16;
     static constexpr int ZP = IY * ZS, XP = XR * XS, GP = YR * GS, GXP = TX * GXS, GYP = TY * GYS;
-    static constexpr int Z_OFF = 0, XS_OFF = 5 * ZP, G_OFF = XS_OFF + 5 * XP, GX_OFF = G_OFF + 3 * GP;
-    static constexpr int GY_OFF = GX_OFF + 3 * GXP;
-    static constexpr int LDS_FLOATS = GY_OFF + 3 * GYP;
-    static constexpr int LDS_FLOATS_LOSS = XS_OFF + 5 * XP;  // forward-only modes
+    // A segment reads rup4(S + 2H) floats from its start; reads past a row's end stay inside the
+    // buffer (the next row or the spare floats) and only feed outputs that are never used.
+    static_assert(SX + rup4(SX + 2 * H) <= ZS + PAD && YR - SY + rup4(SY + 2 * H) <= XS + PAD &&
+                      TX - SA + rup4(SA + 2 * H) <= GS + PAD && TY - SB + rup4(SB + 2 * H) <= GXS + PAD,
+                  "row reads");
+    static constexpr int LDS_FLOATS = 5 * (ZP + XP) + 3 * (GP + GXP + GYP) + 4 * PAD;
     static_assert(LDS_FLOATS * 4 <= 160 * 1024, "LDS");
 };
 

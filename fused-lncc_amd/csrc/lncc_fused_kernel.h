@@ -35,14 +35,17 @@
 
 namespace fl {
 
-// Loads NV consecutive floats from an 8-byte aligned LDS address as float2s.
+// Loads NV consecutive floats from a 16-byte aligned LDS address as float4s (the last one may
+// read up to 3 floats past the row; they are not used).
 template <int NV>
 __device__ __forceinline__ void lds_row(const float* __restrict__ src, float (&v)[NV]) {
 #pragma unroll
-    for (int m = 0; m < NV / 2; ++m) {
-        const float2 f = reinterpret_cast<const float2*>(src)[m];
-        v[2 * m] = f.x;
-        v[2 * m + 1] = f.y;
+    for (int m = 0; m < (NV + 3) / 4; ++m) {
+        const float4 f = reinterpret_cast<const float4*>(src)[m];
+        v[4 * m] = f.x;
+        if (4 * m + 1 < NV) v[4 * m + 1] = f.y;
+        if (4 * m + 2 < NV) v[4 * m + 2] = f.z;
+        if (4 * m + 3 < NV) v[4 * m + 3] = f.w;
     }
 }
 
@@ -71,10 +74,10 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 
     // one __shared__ array per buffer, so the compiler knows that the reads of one stage do not
     // alias the writes of another and can overlap them
-    __shared__ __align__(16) float Zs[5 * G::ZP];
-    __shared__ __align__(16) float Xs[5 * G::XP];
-    __shared__ __align__(16) float Gs[ADJ ? 3 * G::GP : 2];
-    __shared__ __align__(16) float GXs[ADJ ? 3 * G::GXP : 2];
+    __shared__ __align__(16) float Zs[5 * G::ZP + G::PAD];
+    __shared__ __align__(16) float Xs[5 * G::XP + G::PAD];
+    __shared__ __align__(16) float Gs[ADJ ? 3 * G::GP + G::PAD : 4];
+    __shared__ __align__(16) float GXs[ADJ ? 3 * G::GXP + G::PAD : 4];
     __shared__ __align__(16) float GY[ADJ ? 3 * G::GYP : 2];
     __shared__ double red[NT / 64];
 
