@@ -133,12 +133,15 @@ struct Geo {
     static constexpr int SA = 16, ASEG = TX / SA, AITEMS = AY * ASEG;
     // AYs: y-sums of the three; items (ox, seg), outputs oy < TY
     static constexpr int SB = TY / 2, BSEG = TY / SB, BITEMS = TX * BSEG;
-    // Work units of the running-sum passes are single quantities of one segment, spread over all
-    // lanes: phase P1 runs the X units (5 per item) then the AX units (3 per item); phase P0 runs
-    // Y items on the first lanes and the AYs units (3 per item) on the last lanes.
-    static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, U1 = cdiv(UX + UA, NT);
-    static constexpr int UB = 3 * BITEMS, B_LANE0 = NT - UB;
-    static_assert(YITEMS <= NT && UB <= NT, "lanes");
+    // Work units of the running-sum passes are single quantities of one segment. Waves are
+    // spread over the 4 SIMDs of the CU round-robin (wave w on SIMD w % 4), so the heavy items
+    // are placed to even out each SIMD's share of a phase: in phase P1 the X units (5 per item)
+    // fill the first waves and the AX units (3 per item) start on the next wave boundary; in
+    // phase P0 the Y items fill the first waves (SIMDs 0 and 1 get the extra ones) and the AYs
+    // units (3 per item) go to waves 10, 11, 14, 15 (SIMDs 2 and 3), B_PER_WAVE each.
+    static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, AX_LANE0 = rup64(UX), U1 = 1;
+    static constexpr int UB = 3 * BITEMS, B_PER_WAVE = UB / 4;
+    static_assert(YITEMS <= 10 * 64 && AX_LANE0 + UA <= NT && UB % 4 == 0 && B_PER_WAVE <= 64, "lanes");
     // every segment starts on a 16-byte boundary (rows are read as float4)
     static_assert(XR >= AX && TX % SA == 0 && TY % SB == 0 && SX % 4 == 0 && SY % 4 == 0 &&
                       SA % 4 == 0 && SB % 4 == 0, "segments");

@@ -130,8 +130,8 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             u_kind[k] = 1;
             u_src[k] = q * G::ZP + iy * G::ZS + start;
             u_dst[k] = q * G::XP + start * G::XS + iy;
-        } else if (ADJ && u < G::UX + G::UA) {
-            const int v = u - G::UX;
+        } else if (ADJ && u >= G::AX_LANE0 && u < G::AX_LANE0 + G::UA) {
+            const int v = u - G::AX_LANE0;
             const int c = v / G::AITEMS, it = v - c * G::AITEMS;
             const int ay = it % G::AY, start = (it / G::AY) * G::SA;
             u_kind[k] = 2;
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             u_dst[k] = c * G::GXP + start * G::GXS + ay;
         }
     }
-    // P0: Y items on lanes [0, YITEMS), AYs units on lanes [B_LANE0, NT)
+    // P0: Y items on lanes [0, YITEMS), AYs units on waves 10, 11, 14, 15
     const bool has_y = tid < G::YITEMS;
     const int y_ax = has_y ? tid % G::AX : 0;
     const int y_seg = has_y ? tid / G::AX : 0;
@@ -158,10 +158,11 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             y_core[i] = y_inv[i] && corex && ay >= HH && ay < HH + TY;
         }
     }
-    const bool has_b = ADJ && tid >= G::B_LANE0;
+    const int wave = tid >> 6, bslot = wave == 10 ? 0 : wave == 11 ? 1 : wave == 14 ? 2 : wave == 15 ? 3 : -1;
+    const bool has_b = ADJ && bslot >= 0 && (tid & 63) < G::B_PER_WAVE;
     int b_src = 0, b_dst = 0;
     if (has_b) {
-        const int v = tid - G::B_LANE0;
+        const int v = bslot * G::B_PER_WAVE + (tid & 63);
         const int c = v / G::BITEMS, it = v - c * G::BITEMS;
         const int ox = it % TX, start = (it / TX) * G::SB;
         b_src = c * G::GXP + ox * G::GXS + start;
