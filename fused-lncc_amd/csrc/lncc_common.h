@@ -141,7 +141,8 @@ struct Geo {
     // units (3 per item) go to waves 10, 11, 14, 15 (SIMDs 2 and 3), B_PER_WAVE each.
     static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, AX_LANE0 = rup64(UX), U1 = 1;
     static constexpr int UB = 3 * BITEMS, B_PER_WAVE = UB / 4;
-    static_assert(YITEMS <= 10 * 64 && AX_LANE0 + UA <= NT && UB % 4 == 0 && B_PER_WAVE <= 64, "lanes");
+    static_assert(YITEMS <= 10 * 64 && AX_LANE0 + UA <= NT && UB == 192 && B_PER_WAVE == 48 && BSEG == 2 && TX == 32,
+                  "lanes");
     // every segment starts on a 16-byte boundary (rows are read as float4)
     static_assert(XR >= AX && TX % SA == 0 && TY % SB == 0 && SX % 4 == 0 && SY % 4 == 0 &&
                       SA % 4 == 0 && SB % 4 == 0, "segments");

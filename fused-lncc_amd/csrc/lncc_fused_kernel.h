@@ -49,6 +49,28 @@ __device__ __forceinline__ void lds_row(const float* __restrict__ src, float (&v
     }
 }
 
+// Lane order for work over n_rows rows of LEN (>= 32) positions: indices [0, 32 n_rows) take
+// positions 0..31 of one row per 32 consecutive lanes, so that each half-wave stores into a
+// single destination row (consecutive LDS banks, no conflicts); the remaining indices take
+// positions 32..LEN-1 row after row.
+template <int LEN>
+__device__ __forceinline__ void split32(int idx, int n_rows, int& row, int& pos) {
+    static_assert(LEN >= 32, "rows of at least 32 positions");
+    if constexpr (LEN == 32) {
+        row = idx >> 5;
+        pos = idx & 31;
+    } else {
+        if (idx < 32 * n_rows) {
+            row = idx >> 5;
+            pos = idx & 31;
+        } else {
+            const int e = idx - 32 * n_rows;
+            row = e / (LEN - 32);
+            pos = 32 + e % (LEN - 32);
+        }
+    }
+}
+
 // Running window sums of width 2H+1: out[i] = v[i] + ... + v[i+2H] for i < S.
 template <int H, int S>
 __device__ __forceinline__ void window_sums(const float (&v)[S + 2 * H], float (&out)[S]) {
@@ -124,16 +146,16 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
         u_src[k] = 0;
         u_dst[k] = 0;
         if (u < G::UX) {
-            const int q = u / G::XITEMS, it = u - q * G::XITEMS;
-            const int iy = it % G::IY, seg = it / G::IY;
-            const int start = seg * G::SX;
+            int row, iy;  // rows (q, seg) of IY positions
+            split32<G::IY>(u, 5 * G::XSEG, row, iy);
+            const int q = row / G::XSEG, start = (row % G::XSEG) * G::SX;
             u_kind[k] = 1;
             u_src[k] = q * G::ZP + iy * G::ZS + start;
             u_dst[k] = q * G::XP + start * G::XS + iy;
         } else if (ADJ && u >= G::AX_LANE0 && u < G::AX_LANE0 + G::UA) {
-            const int v = u - G::AX_LANE0;
-            const int c = v / G::AITEMS, it = v - c * G::AITEMS;
-            const int ay = it % G::AY, start = (it / G::AY) * G::SA;
+            int row, ay;  // rows (c, seg) of AY positions
+            split32<G::AY>(u - G::AX_LANE0, 3 * G::ASEG, row, ay);
+            const int c = row / G::ASEG, start = (row % G::ASEG) * G::SA;
             u_kind[k] = 2;
             u_src[k] = c * G::GP + ay * G::GS + start;
             u_dst[k] = c * G::GXP + start * G::GXS + ay;
@@ -141,8 +163,8 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     }
     // P0: Y items on lanes [0, YITEMS), AYs units on waves 10, 11, 14, 15
     const bool has_y = tid < G::YITEMS;
-    const int y_ax = has_y ? tid % G::AX : 0;
-    const int y_seg = has_y ? tid / G::AX : 0;
+    int y_seg = 0, y_ax = 0;  // rows seg of AX positions
+    if (has_y) split32<G::AX>(tid, G::YSEG, y_seg, y_ax);
     const int y_start = y_seg * G::SY;
     // per output of the Y segment: inside the volume (ncc and adjoints live) / counted in the loss
     // (inside the volume and in the output tile); the same on every plane
@@ -162,9 +184,12 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const bool has_b = ADJ && bslot >= 0 && (tid & 63) < G::B_PER_WAVE;
     int b_src = 0, b_dst = 0;
     if (has_b) {
-        const int v = bslot * G::B_PER_WAVE + (tid & 63);
-        const int c = v / G::BITEMS, it = v - c * G::BITEMS;
-        const int ox = it % TX, start = (it / TX) * G::SB;
+        // rows (c, seg) of TX = 32 positions: slot s takes row s on its first 32 lanes and half
+        // of row 4 + s/2 on the next 16
+        const int l = tid & 63;
+        const int row = l < 32 ? bslot : 4 + (bslot >> 1);
+        const int ox = l < 32 ? l : (bslot & 1) * 16 + (l - 32);
+        const int c = row / G::BSEG, start = (row % G::BSEG) * G::SB;
         b_src = c * G::GXP + ox * G::GXS + start;
         b_dst = c * G::GYP + start * G::GYS + ox;
     }
