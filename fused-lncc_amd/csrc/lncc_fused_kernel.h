@@ -256,12 +256,13 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             const int zcY = zi - 1 - HH;
             const bool actY = zcY >= zc_lo && zcY < zc_hi;
             if (actY && has_y) {
-                // all five rows are read before any arithmetic, so their LDS latencies overlap
-                float yv[5][G::SY + 2 * HH], S[5][G::SY];
+                float S[5][G::SY];
 #pragma unroll
-                for (int q = 0; q < 5; ++q) lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv[q]);
-#pragma unroll
-                for (int q = 0; q < 5; ++q) window_sums<HH, G::SY>(yv[q], S[q]);
+                for (int q = 0; q < 5; ++q) {
+                    float yv[G::SY + 2 * HH];
+                    lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv);
+                    window_sums<HH, G::SY>(yv, S[q]);
+                }
                 const bool count = zcY >= z0 && zcY < z1;
                 float lsum = 0.f;
 #pragma unroll
