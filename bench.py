@@ -32,7 +32,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
-    ap.add_argument("--warmup", type=int, default=12)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="headline", choices=["headline", "bf16", "mri", "large"])
     ap.add_argument("--kernel-reps", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -131,13 +131,14 @@ def main():
     grad = torch.empty_like(p)
     stream = torch.cuda.current_stream(dev)
     kev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * a.kernel_reps)]
-    for i in range(a.kernel_reps + 3):
-        if i >= 3:
-            kev[2 * (i - 3)].record(stream)
+    kwarm = 10
+    for i in range(a.kernel_reps + kwarm):
+        if i >= kwarm:
+            kev[2 * (i - kwarm)].record(stream)
         _lib.check(lib.fl_lncc_fused_partials(p.data_ptr(), t.data_ptr(), code, B, D, H, W, k, 1e-5,
                                               grad.data_ptr(), ws.data_ptr(), nbytes, stream.cuda_stream))
-        if i >= 3:
-            kev[2 * (i - 3) + 1].record(stream)
+        if i >= kwarm:
+            kev[2 * (i - kwarm) + 1].record(stream)
     torch.cuda.synchronize()
     kms = [kev[2 * i].elapsed_time(kev[2 * i + 1]) for i in range(a.kernel_reps)]
     kernel_ms = sum(kms) / len(kms)
