@@ -4,7 +4,8 @@
 * fl_validate rejects what the reference rejects (fused_lncc/csrc/lncc3d.cu:123,128-129,158,
   255-260,281; fused_lncc/__init__.py:81-82) before any device work;
 * the Python API raises the reference's exception types;
-* the fake (meta) kernels give torch.compile the right dtypes;
+* the fake (meta) kernels give torch.compile the right dtypes, and the loss with its backward
+  traces on fake tensors;
 * the product package never imports the oracle.
 """
 import ast
@@ -105,6 +106,29 @@ def test_fake_kernels_dtypes():
             assert len(outs) == 4 and all(o.dtype == torch.float32 for o in outs)
             g = torch.ops.fused_lncc.backward(outs[1], outs[2], outs[3], pf, pf, 7, 1.0)
             assert g.dtype == dt
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_fake_trace_of_loss_and_backward(dt):
+    """The autograd function traces end to end on fake tensors (what torch.compile does before any
+    kernel runs): a float32 0-d loss, a gradient in the pred dtype, and the custom ops in the graph."""
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    def step(p, t):
+        loss = fused_lncc_loss(p, t, 5)
+        (g,) = torch.autograd.grad(2.0 * loss, p)
+        return loss, g
+
+    p = torch.randn(1, 2, 8, 9, 10, dtype=dt, requires_grad=True)
+    t = torch.randn(1, 2, 8, 9, 10, dtype=dt)
+    gm = make_fx(step, tracing_mode="fake")(p, t)
+    ops = {str(n.target) for n in gm.graph.nodes if n.op == "call_function"}
+    assert any("fused_lncc.loss_grad" in o for o in ops), ops
+    assert any("fused_lncc.scale_grad_" in o for o in ops), ops
+    outs = [n for n in gm.graph.nodes if n.op == "output"][0].args[0]
+    loss_meta, g_meta = outs[0].meta["val"], outs[1].meta["val"]
+    assert loss_meta.dtype == torch.float32 and loss_meta.shape == ()
+    assert g_meta.dtype == dt and g_meta.shape == p.shape
 
 
 def test_product_never_imports_the_oracle():
