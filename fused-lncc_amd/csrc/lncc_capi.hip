@@ -39,14 +39,24 @@ Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     p.ntx = (int)((W + fl::TX - 1) / fl::TX);
     p.nty = (int)((H + ty - 1) / ty);
     const int64_t base = B * p.ntx * p.nty;
-    const int64_t target = 512;
+    // Split D into nzc chunks. A chunk of d planes costs d + 4h + 2 pipeline steps, and the
+    // workgroups run in rounds of one per CU (MI355X: 256 CUs): pick the split with the fewest
+    // rounds x steps (ties: fewer workgroups).
+    const int64_t kCUs = 256;
     const int64_t minchunk = 4 * halo > 8 ? 4 * halo : 8;
-    int64_t nzc = (target + base - 1) / base;
     int64_t maxz = D / minchunk;
     if (maxz < 1) maxz = 1;
-    if (nzc > maxz) nzc = maxz;
-    if (nzc < 1) nzc = 1;
-    int64_t dchunk = (D + nzc - 1) / nzc;
+    int64_t best_cost = -1, dchunk = D;
+    for (int64_t nzc = 1; nzc <= maxz; ++nzc) {
+        const int64_t d = (D + nzc - 1) / nzc;
+        const int64_t blocks = base * ((D + d - 1) / d);
+        const int64_t cost = ((blocks + kCUs - 1) / kCUs) * (d + 4 * halo + 2);
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            dchunk = d;
+        }
+        if (blocks >= 8 * kCUs) break;
+    }
     if (const char* e = getenv("FUSED_LNCC_DCHUNK")) {
         const long v = strtol(e, nullptr, 10);
         if (v > 0) dchunk = v < D ? v : D;
