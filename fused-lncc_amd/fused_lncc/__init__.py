@@ -76,6 +76,12 @@ def _compiling():
         return False
 
 
+def _traced(t):
+    """True under torch.compile or any fake-tensor trace: the custom ops (with their fake kernels)
+    must then stand in for the library calls. Eager calls skip the op dispatch (~20 us each)."""
+    return _compiling() or torch._guards.detect_fake_mode((t,)) is not None
+
+
 class _FusedLNCC(torch.autograd.Function):
     """Autograd wrapper: the gradient is produced in forward by the fused kernel and handed out in
     backward (fused_lncc/__init__.py:49-74 computes it in backward from four saved fp32 maps)."""
@@ -87,11 +93,16 @@ class _FusedLNCC(torch.autograd.Function):
         pf = pred.reshape(N * C, *S)
         tf = target.reshape(N * C, *S)
         need = bool(need_grad and ctx.needs_input_grad[0])
-        loss, grad = torch.ops.fused_lncc.loss_grad(pf, tf, kernel_size, smooth_dr, need)
+        traced = _traced(pf)
+        if traced:
+            loss, grad = torch.ops.fused_lncc.loss_grad(pf, tf, kernel_size, smooth_dr, need)
+        else:
+            loss, grad = ext.loss_grad(pf, tf, kernel_size, smooth_dr, need)
         ctx.k = kernel_size
         ctx.dr = smooth_dr
         ctx.shape = pred.shape
         ctx.grad = None
+        ctx.traced = traced
         if need:
             if _compiling():
                 ctx.save_for_backward(pf, tf, grad)
@@ -111,9 +122,14 @@ class _FusedLNCC(torch.autograd.Function):
             return g.reshape(ctx.shape), None, None, None, None
         g = ctx.grad
         ctx.grad = None
-        if g is None:  # second backward through a retained graph: recompute
-            _, g = torch.ops.fused_lncc.loss_grad(pf, tf, ctx.k, ctx.dr, True)
-        torch.ops.fused_lncc.scale_grad_(g, grad_out.detach())
+        if ctx.traced:
+            if g is None:  # second backward through a retained graph: recompute
+                _, g = torch.ops.fused_lncc.loss_grad(pf, tf, ctx.k, ctx.dr, True)
+            torch.ops.fused_lncc.scale_grad_(g, grad_out.detach())
+        else:
+            if g is None:
+                _, g = ext.loss_grad(pf, tf, ctx.k, ctx.dr, True)
+            ext.scale_grad_(g, grad_out)
         return g.reshape(ctx.shape), None, None, None, None
 
 

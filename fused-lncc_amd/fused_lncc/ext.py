@@ -33,26 +33,52 @@ def _stream(dev):
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+class _on_device:
+    """Makes `dev` the current device for the C ABI call (its stream must belong to it); a no-op,
+    without the cost of torch.cuda.device's context switch, when it already is."""
+
+    __slots__ = ("dev", "prev")
+
+    def __init__(self, dev):
+        self.dev = dev.index if dev.index is not None else torch.cuda.current_device()
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.dev:
+            self.prev = cur
+            torch.cuda.set_device(self.dev)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
 def workspace_bytes(shape, kernel_size):
     B, D, H, W = shape
     return int(_lib.load().fl_workspace_bytes(B, D, H, W, int(kernel_size)))
 
 
 def loss_grad(pf, tf, kernel_size, smooth_dr, need_grad=True):
-    """Fused forward (+ gradient wrt pf, already multiplied by -1/M). Returns (loss, grad|None)."""
+    """Fused forward (+ gradient wrt pf, already multiplied by -1/M). Returns (loss, grad|None).
+    Shape, k and dtype are validated by the C ABI before any device work."""
     code = _dtype_code(pf)
     _check4d("pred", pf)
     _check4d("target", tf, like=pf, dtype=pf.dtype)
     lib = _lib.load()
     B, D, H, W = pf.shape
-    _lib.check(lib.fl_validate(code, int(kernel_size), B, D, H, W))
-    with torch.cuda.device(pf.device):
-        nbytes = lib.fl_workspace_bytes(B, D, H, W, int(kernel_size))
+    k = int(kernel_size)
+    with _on_device(pf.device):
+        nbytes = lib.fl_workspace_bytes(B, D, H, W, k)
+        if nbytes == 0:  # an invalid k or shape: let fl_validate name it
+            _lib.check(lib.fl_validate(code, k, B, D, H, W))
         ws = torch.empty(nbytes, dtype=torch.uint8, device=pf.device)
         loss = torch.empty((), dtype=torch.float32, device=pf.device)
         grad = torch.empty_like(pf) if need_grad else None
         _lib.check(lib.fl_lncc_loss_grad(
-            pf.data_ptr(), tf.data_ptr(), code, B, D, H, W, int(kernel_size), float(smooth_dr),
+            pf.data_ptr(), tf.data_ptr(), code, B, D, H, W, k, float(smooth_dr),
             loss.data_ptr(), grad.data_ptr() if grad is not None else None, ws.data_ptr(), nbytes,
             _stream(pf.device)))
     return loss, grad
@@ -61,8 +87,10 @@ def loss_grad(pf, tf, kernel_size, smooth_dr, need_grad=True):
 def scale_grad_(grad, grad_out):
     """In place: grad *= grad_out (0-d float32 device tensor), skipped on the device when it is 1."""
     code = _dtype_code(grad)
-    go = grad_out.detach().to(device=grad.device, dtype=torch.float32).contiguous()
-    with torch.cuda.device(grad.device):
+    go = grad_out.detach()
+    if go.dtype != torch.float32 or go.device != grad.device:
+        go = go.to(device=grad.device, dtype=torch.float32)
+    with _on_device(grad.device):
         _lib.check(_lib.load().fl_scale_grad(grad.data_ptr(), code, grad.numel(), go.data_ptr(),
                                              _stream(grad.device)))
     return grad
