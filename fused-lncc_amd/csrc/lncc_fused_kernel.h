@@ -5,9 +5,10 @@
 // along D so that every quantity is produced from data already on chip:
 //
 //   F   (registers) lanes own the input columns of the (TX+4h) x (TY+4h) region and keep running
-//       z-sums of p, t, p^2, t^2, p*t: add plane zi, subtract plane zi-k (re-read from global
-//       memory, where it is still cache-resident, rather than held in a register ring; both are
-//       prefetched one plane ahead); write the five z-sums to LDS.
+//       z-sums of p, t, p^2, t^2, p*t: add plane zi (prefetched one plane ahead), subtract plane
+//       zi-k (from a k-deep register ring of p,t; for k = 9, where the ring does not fit the
+//       register budget, re-read from global memory, still cache resident, and prefetched too);
+//       write the five z-sums to LDS.
 //   X   running x-sums of the five z-sums over the (TX+2h)-wide adjoint range.
 //   Y   running y-sums -> the five k^3 box-sums on the (TX+2h) x (TY+2h) adjoint region; per voxel
 //       squared NCC (clamped to 1), loss partial sums, and the adjoint coefficients alpha, beta,
@@ -204,13 +205,23 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const int zc_lo = ADJ ? max(z0 - HH, 0) : z0;
     const int zc_hi = ADJ ? min(z1 + HH, D) : z1;
 
-    // F state: running z-sums; p,t of the next plane and of the plane leaving the window (prefetched)
-    float zsum[J][5], pnext[J], tnext[J], pold[J], told[J];
+    // F state: running z-sums; p,t of the next plane (prefetched one step ahead); the plane leaving
+    // the window comes from a k-deep register ring of the last k planes' p,t (k <= 7) or, where
+    // the ring would not fit in the register budget (k = 9), is re-read from global memory (still
+    // cache resident) and prefetched like the new plane
+    constexpr bool RING = K <= 7;
+    constexpr int KR = RING ? K : 1;
+    float zsum[J][5], pnext[J], tnext[J], pring[KR][J], tring[KR][J], pold[J], told[J];
     float pz = 0.f, tzz = 0.f;  // AZ: p,t at this step's output plane (prefetched one step ahead)
 #pragma unroll
     for (int j = 0; j < J; ++j) {
 #pragma unroll
         for (int q = 0; q < 5; ++q) zsum[j][q] = 0.f;
+#pragma unroll
+        for (int r = 0; r < KR; ++r) {
+            pring[r][j] = 0.f;
+            tring[r][j] = 0.f;
+        }
         pold[j] = 0.f;
         told[j] = 0.f;
     }
@@ -322,7 +333,19 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             {
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
-                    const float p = pnext[j], t = tnext[j], po = pold[j], to = told[j];
+                    // plane zi replaces plane zi-k (ring slot r; the ring starts at zero: nothing
+                    // before the first plane of the march was added)
+                    const float p = pnext[j], t = tnext[j];
+                    float po, to;
+                    if constexpr (RING) {
+                        po = pring[r][j];
+                        to = tring[r][j];
+                        pring[r][j] = p;
+                        tring[r][j] = t;
+                    } else {
+                        po = pold[j];
+                        to = told[j];
+                    }
                     zsum[j][0] += p - po;
                     zsum[j][1] += t - to;
                     zsum[j][2] = fmaf(p, p, fmaf(-po, po, zsum[j][2]));
@@ -333,18 +356,24 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                         for (int q = 0; q < 5; ++q) Zs[q * G::ZP + zaddr[j]] = zsum[j][q];
                     }
                 }
-                // prefetch plane zi+1 and plane zi+1-k (leaving the window)
-                const bool okn = zi + 1 < zn_hi, okq = zi >= zq_lo && zi < zq_hi;
+                // prefetch plane zi+1 (and, without the ring, plane zi+1-k leaving the window)
+                const bool okn = zi + 1 < zn_hi;
                 const __amdgpu_buffer_rsrc_t rpn = rsrc_at(pva + zoff + PB, plane_bytes, okn);
                 const __amdgpu_buffer_rsrc_t rtn = rsrc_at(tva + zoff + PB, plane_bytes, okn);
-                const __amdgpu_buffer_rsrc_t rpq = rsrc_at(pva + zoff - (K - 1) * PB, plane_bytes, okq);
-                const __amdgpu_buffer_rsrc_t rtq = rsrc_at(tva + zoff - (K - 1) * PB, plane_bytes, okq);
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
                     pnext[j] = load_elem<BF16>(rpn, voff[j]);
                     tnext[j] = load_elem<BF16>(rtn, voff[j]);
-                    pold[j] = load_elem<BF16>(rpq, voff[j]);
-                    told[j] = load_elem<BF16>(rtq, voff[j]);
+                }
+                if constexpr (!RING) {
+                    const bool okq = zi >= zq_lo && zi < zq_hi;
+                    const __amdgpu_buffer_rsrc_t rpq = rsrc_at(pva + zoff - (K - 1) * PB, plane_bytes, okq);
+                    const __amdgpu_buffer_rsrc_t rtq = rsrc_at(tva + zoff - (K - 1) * PB, plane_bytes, okq);
+#pragma unroll
+                    for (int j = 0; j < J; ++j) {
+                        pold[j] = load_elem<BF16>(rpq, voff[j]);
+                        told[j] = load_elem<BF16>(rtq, voff[j]);
+                    }
                 }
             }
             __syncthreads();
