@@ -194,6 +194,19 @@ def test_many_volumes():
     assert_grad(g, gr)
 
 
+@pytest.mark.parametrize("k", [3, 7, 9])
+@pytest.mark.parametrize("dchunk", [1, 3, 8])
+def test_d_chunk_seams(k, dchunk, monkeypatch):
+    """Workgroups that own short D chunks restart the running z-sums at every chunk: forcing the
+    chunk length (FUSED_LNCC_DCHUNK, read at each launch) puts many seams into one volume."""
+    monkeypatch.setenv("FUSED_LNCC_DCHUNK", str(dchunk))
+    p, t = wl.randn_pair((1, 2, 37, 30, 41), 40 + k)
+    loss, g, _ = fused(p, t, k)
+    lr, gr = O.lncc(p.numpy(), t.numpy(), k)
+    assert_loss(loss, lr, LOSS_RTOL_F32)
+    assert_grad(g, gr)
+
+
 def test_unsupported_dtype_raises():
     p = torch.randn(1, 1, 16, 16, 16, device=DEV, dtype=torch.float64)
     with pytest.raises(RuntimeError):
