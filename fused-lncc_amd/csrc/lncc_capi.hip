@@ -193,7 +193,9 @@ int fl_lncc_maps(const void* pred, const void* target, int dtype, int64_t B, int
                  int kernel_size, float smooth_dr, float* ncc, float* A, float* Bc, float* Cc, void* stream) {
     int rc = fl_validate(dtype, kernel_size, B, D, H, W);
     if (rc) return rc;
-    if (!pred || !target || !ncc || !A || !Bc || !Cc) return fail(FL_E_NULL, "fl_lncc_maps: NULL pointer argument");
+    const bool adjoint_maps = A || Bc || Cc;
+    if (!pred || !target || !ncc || (adjoint_maps && !(A && Bc && Cc)))
+        return fail(FL_E_NULL, "fl_lncc_maps: NULL pointer argument (A, Bc, Cc are all given or all NULL)");
     const int halo = kernel_size / 2;
     const Plan p = plan_fused(B, D, H, W, halo);
     fl::FusedArgs a = {};

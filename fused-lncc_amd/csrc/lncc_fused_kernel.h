@@ -306,9 +306,11 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                             const int gx = x0 - HH + y_ax, gy = y0 - HH + ay;
                             const int64_t o = ((b * D + zcY) * Hd + gy) * (int64_t)Wd + gx;
                             a.ncc_map[o] = nccc;
-                            a.a_map[o] = live ? -2.f * inv_n * (cr * w) : 0.f;
-                            a.b_map[o] = live ? -(cr * uu) : 0.f;
-                            a.c_map[o] = live ? 2.f * cr : 0.f;
+                            if (a.a_map) {  // null: the ncc map alone
+                                a.a_map[o] = live ? -2.f * inv_n * (cr * w) : 0.f;
+                                a.b_map[o] = live ? -(cr * uu) : 0.f;
+                                a.c_map[o] = live ? 2.f * cr : 0.f;
+                            }
                         }
                     }
                 }

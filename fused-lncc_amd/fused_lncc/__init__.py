@@ -17,7 +17,7 @@ import torch
 
 from . import _lib, ext
 
-__all__ = ["fused_lncc_loss", "ext"]
+__all__ = ["fused_lncc_loss", "lncc_map", "ext"]
 
 
 # Custom ops keep the loss traceable by torch.compile (fused_lncc/__init__.py:22-46). Fake kernels
@@ -144,3 +144,16 @@ def fused_lncc_loss(pred, target, kernel_size=7, smooth_dr=1e-5):
     # no_grad or for a pred without requires_grad the kernel reads 8 B/voxel and writes nothing.
     need_grad = torch.is_grad_enabled() and pred.requires_grad
     return _FusedLNCC.apply(pred.contiguous(), target.contiguous(), kernel_size, smooth_dr, need_grad)
+
+
+def lncc_map(pred, target, kernel_size=7, smooth_dr=1e-5):
+    """Per-voxel squared local NCC (clamped to 1), float32, shape of ``pred``: the similarity map
+    whose mean is ``1 - fused_lncc_loss`` (the evaluation output of the reference's roadmap,
+    reduction='none'). Forward only: the map is not differentiable through this call."""
+    assert pred.dim() == 5 and pred.shape == target.shape, "expect matching (N,C,D,H,W)"
+    assert kernel_size % 2 == 1, "kernel_size must be odd"
+    N, C = pred.shape[:2]
+    S = pred.shape[2:]
+    pf = pred.detach().contiguous().reshape(N * C, *S)
+    tf = target.detach().contiguous().reshape(N * C, *S)
+    return ext.ncc_map(pf, tf, kernel_size, smooth_dr).reshape(pred.shape)

@@ -111,6 +111,22 @@ def lncc_forward(P, T, kernel_size, dr):
     return outs
 
 
+def ncc_map(P, T, kernel_size, dr):
+    """The per-voxel (clamped) squared local NCC of (B,D,H,W) inputs, float32 — the first output of
+    lncc_forward without the three adjoint maps."""
+    code = _dtype_code(P)
+    _check4d("P", P)
+    _check4d("T", T, like=P, dtype=P.dtype)
+    lib = _lib.load()
+    B, D, H, W = P.shape
+    _lib.check(lib.fl_validate(code, int(kernel_size), B, D, H, W))
+    out = torch.empty(P.shape, dtype=torch.float32, device=P.device)
+    with _on_device(P.device):
+        _lib.check(lib.fl_lncc_maps(P.data_ptr(), T.data_ptr(), code, B, D, H, W, int(kernel_size),
+                                    float(dr), out.data_ptr(), None, None, None, _stream(P.device)))
+    return out
+
+
 def lncc_backward(A, Bc, Cc, P, T, kernel_size, scale):
     """scale * (box A + 2P box Bc + T box Cc) in P's dtype — fused_lncc/csrc/lncc3d.cu:253-284."""
     _check4d("A", A, dtype=torch.float32)

@@ -83,7 +83,10 @@ int fl_scale_grad(void* grad, int dtype, int64_t n, const float* grad_out, void*
 
 /*
  * Per-voxel maps ncc (clamped), A = dncc/dSp, Bc = dncc/dvar_p, Cc = dncc/dcross as float32,
- * each (B,D,H,W) — the outputs of lncc_forward, fused_lncc/csrc/lncc3d.cu:127-161. Debug/test path.
+ * each (B,D,H,W) — the outputs of lncc_forward, fused_lncc/csrc/lncc3d.cu:127-161. A, Bc and Cc
+ * may all be NULL: then only the ncc map is written (4 B per voxel; the per-voxel similarity of
+ * the evaluation path, examples/registration_demo.py:59-63, and the map checked in
+ * tests/verify_fwd.py:21-34).
  */
 int fl_lncc_maps(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H, int64_t W,
                  int kernel_size, float smooth_dr, float* ncc, float* A, float* Bc, float* Cc, void* stream);

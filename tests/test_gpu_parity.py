@@ -147,6 +147,26 @@ def test_maps_match_oracle(k, shape):
         assert np.linalg.norm(got - om[key]) / np.linalg.norm(om[key]) < 1e-3, key
 
 
+@pytest.mark.parametrize("k", [3, 7])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_lncc_map(k, dtype):
+    """The ncc map alone (no adjoint maps): equal to lncc_forward's first output, close to the
+    oracle's map, and its mean is 1 - loss."""
+    from fused_lncc import lncc_map
+    shape = (2, 3, 18, 21, 26)
+    p, t = wl.randn_pair(shape, 70 + k)
+    pd, td = p.to(dtype).to(DEV), t.to(dtype).to(DEV)
+    m = lncc_map(pd, td, k)
+    assert m.shape == shape and m.dtype == torch.float32
+    ref = ext.lncc_forward(pd.reshape(6, *shape[2:]), td.reshape(6, *shape[2:]), k, 1e-5)[0]
+    assert torch.equal(m.reshape(ref.shape), ref)
+    loss = fused_lncc_loss(pd, td, k)
+    assert abs((1.0 - m.double().mean().item()) - loss.item()) <= 1e-5 * abs(loss.item())
+    if dtype == torch.float32:
+        _, _, om = O.lncc(p.numpy(), t.numpy(), k, grad=False, maps=True)
+        assert np.abs(m.double().cpu().numpy() - om["ncc"]).max() < 1e-3
+
+
 @pytest.mark.parametrize("k", [3, 5, 7, 9])
 def test_box3d_matches_oracle(k):
     x = torch.randn(3, 13, 17, 11, generator=torch.Generator().manual_seed(k))

@@ -68,6 +68,9 @@ def test_errors_before_device_work():
     # a workspace that is too small is refused
     rc = lib.fl_lncc_loss_grad(8, 8, 0, 1, 8, 8, 8, 7, 1e-5, 8, None, 8, 0, None)
     assert rc == _lib.FL_E_WORKSPACE
+    # the adjoint maps are all given or all omitted
+    rc = lib.fl_lncc_maps(8, 8, 0, 1, 8, 8, 8, 7, 1e-5, 8, 8, None, 8, None)
+    assert rc == _lib.FL_E_NULL and "all NULL" in lib.fl_last_error().decode()
 
 
 def test_workspace_bytes():
