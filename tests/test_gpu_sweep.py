@@ -1,0 +1,55 @@
+"""Randomized parity sweep: many small shapes (edges smaller than the halo, one-plane volumes,
+ragged tiles), every kernel size, both dtypes, against the CPU oracle with the north-star bar.
+Seeded, so every run draws the same cases; each case prints its parameters on failure."""
+import random
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import workloads as wl
+from fused_lncc import fused_lncc_loss
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases(n=60, seed=11):
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        k = rng.choice([3, 5, 7, 9])
+        shape = (rng.randint(1, 2), rng.randint(1, 2), rng.randint(1, 36), rng.randint(1, 66), rng.randint(1, 66))
+        dt = rng.choice(["f32", "f32", "bf16"])
+        corr = rng.random() < 0.3
+        out.append((i, k, shape, dt, corr))
+    return out
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: f"{c[0]}-k{c[1]}-{'x'.join(map(str, c[2]))}-{c[3]}")
+def test_random_shapes(case):
+    i, k, shape, dt, corr = case
+    p, t = wl.randn_pair(shape, 500 + i)
+    if corr:
+        p = 0.8 * t + 0.2 * p
+    dtype = torch.float32 if dt == "f32" else torch.bfloat16
+    pq, tq = p.to(dtype), t.to(dtype)
+    pd = pq.to("cuda").requires_grad_(True)
+    loss = fused_lncc_loss(pd, tq.to("cuda"), k)
+    loss.backward()
+    torch.cuda.synchronize()
+    lr, gr = O.lncc(pq.float().numpy(), tq.float().numpy(), k)
+    assert pd.grad.dtype == dtype
+    g = pd.grad.double().cpu().numpy().ravel()
+    gr = np.asarray(gr, np.float64).ravel()
+    assert abs(loss.item() - lr) <= (1e-5 if dt == "f32" else 1e-2) * abs(lr)
+    n = np.linalg.norm(gr)
+    if n == 0:
+        assert np.linalg.norm(g) == 0
+        return
+    cos = float(g @ gr / (np.linalg.norm(g) * n))
+    rel = float(np.linalg.norm(g - gr) / n)
+    if dt == "f32":
+        assert cos > 0.9999 and rel < 1e-3, (cos, rel)
+    else:  # the gradient is rounded once to bf16 (8 significant bits)
+        assert cos > 0.999 and rel < 2e-2, (cos, rel)
