@@ -53,6 +53,17 @@ def copy_probe():
     print(json.dumps({"copy_probe_bytes_read": x.numel() * 4, "copy_probe_bytes_written": y.numel() * 4}))
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
 def cpu_baseline(k, seconds):
     import torch
 
@@ -75,7 +86,7 @@ def cpu_baseline(k, seconds):
             "kind": "port",
             "sample": f"1 of the 32 volumes, (1,1,128,128,128) fp32 k=7, loss + grad wrt pred; "
                       f"median of {len(times)} runs = {med * 1e3:.1f} ms "
-                      f"({vox / med / 1e6:.3f} Mvoxel/s) on {torch.get_num_threads()} threads"}
+                      f"({vox / med / 1e6:.3f} Mvoxel/s) on {torch.get_num_threads()} threads of {_cpu_model()}"}
 
 
 def main():
