@@ -42,14 +42,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_at(uint64_t addr, uint32_
     return make_rsrc((const void*)(uintptr_t)addr, valid ? bytes : 0u);
 }
 
-template <bool BF16>
+// Cache-policy operand of the buffer instructions: 0 = default, kNT = non-temporal (the line is
+// streamed: a store does not displace data that will be read again from the L2, a load marks the
+// line as the first to evict).
+constexpr int kNT = 2;
+
+template <bool BF16, int AUX = 0>
 __device__ __forceinline__ float load_elem(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
     if constexpr (BF16) {
-        uint32_t u = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, 0, 0);
+        uint32_t u = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, 0, AUX);
         return __uint_as_float(u << 16);
     } else {
         // the builtin returns the raw 32 bits; reinterpret, do not convert
-        return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0));
+        return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, AUX));
     }
 }
 
@@ -70,12 +75,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
     return (uint16_t)(u >> 16);
 }
 
-template <bool BF16>
+template <bool BF16, int AUX = 0>
 __device__ __forceinline__ void store_elem_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, float v) {
     if constexpr (BF16) {
-        __builtin_amdgcn_raw_buffer_store_b16((unsigned short)f32_to_bf16_bits(v), r, (int)voff, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16((unsigned short)f32_to_bf16_bits(v), r, (int)voff, 0, AUX);
     } else {
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)voff, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)voff, 0, AUX);
     }
 }
 

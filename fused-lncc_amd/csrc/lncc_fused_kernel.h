@@ -16,8 +16,8 @@
 //   AX  running x-sums of alpha, beta, gamma over the TX output columns.
 //   AYs running y-sums of the three over the TY output rows.
 //   AZ  (registers) one lane per output column: k-deep ring of the xy-sums and running z-sums ->
-//       box(alpha), box(beta), box(gamma), combined with p,t of the output plane (re-read, cache
-//       resident) into the gradient, the only per-voxel write to HBM.
+//       box(alpha), box(beta), box(gamma), combined with p,t of the output plane (re-read from
+//       the L2 as their last use, non-temporal) into the gradient, the only per-voxel write to HBM.
 //
 // Software pipeline: the chain F -> X -> Y -> AX -> AYs -> AZ alternates between two phases per
 // plane, P0 = {F(zi), Y(zi-1), AYs(zi-2)} and P1 = {X(zi), AX(zi-1), AZ(zi-2)}, so each plane costs
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     window_sums<HH, G::SY>(yv, S[q]);
                 }
                 const bool count = zcY >= z0 && zcY < z1;
-                float lsum = 0.f;
+                float lsum = -0.f;  // -0 + x == x for every x, so the first add folds away
 #pragma unroll
                 for (int i = 0; i < G::SY; ++i) {
                     const int ay = y_start + i;
@@ -415,12 +415,20 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     }
                     const int zo = zi - ZO;
                     const float g = a.gscale * fmaf(inv_n, gz[0], fmaf(pz, gz[1], -tzz * gz[2]));
-                    store_elem_buf<BF16>(rsrc_at(gva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, g);
+                    // Non-temporal: the gradient is never read back, and this re-read of p,t is the
+                    // last use of those lines. With the default policy both would be promoted in the
+                    // L2 and push out the planes that F loaded and this stage re-reads 2h+2 steps
+                    // later, so that every input byte would be fetched about twice; marked
+                    // evict-first, every input byte is fetched from HBM once. bf16 gradient rows
+                    // of a tile are half a 128-byte line (the x-neighbour tile writes the other
+                    // half): those stores keep the default policy, so that the L2 merges the two
+                    // halves into one write.
+                    store_elem_buf<BF16, BF16 ? 0 : kNT>(rsrc_at(gva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, g);
                     // prefetch p,t at the next step's output plane; issued after this step's use, so
                     // one register each suffices and no copy has to wait for the load
                     const bool oko = zo + 1 >= z0 && zo + 1 < z1;
-                    pz = load_elem<BF16>(rsrc_at(pva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
-                    tzz = load_elem<BF16>(rsrc_at(tva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
+                    pz = load_elem<BF16, kNT>(rsrc_at(pva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
+                    tzz = load_elem<BF16, kNT>(rsrc_at(tva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
                 }
             }
             zoff += PB;
