@@ -77,9 +77,13 @@ def _compiling():
 
 
 def _traced(t):
-    """True under torch.compile or any fake-tensor trace: the custom ops (with their fake kernels)
-    must then stand in for the library calls. Eager calls skip the op dispatch (~20 us each)."""
-    return _compiling() or torch._guards.detect_fake_mode((t,)) is not None
+    """True under torch.compile, any dispatch-mode trace (fake tensors, make_fx) or a fake-tensor
+    input: the custom ops (with their fake kernels) then stand in for the library calls, so that
+    the trace records them. Eager calls on plain tensors skip the op dispatch (~20 us each) and the
+    fake-mode search (~5 us)."""
+    if _compiling() or torch._C._len_torch_dispatch_stack() > 0:
+        return True
+    return type(t) is not torch.Tensor and torch._guards.detect_fake_mode((t,)) is not None
 
 
 class _FusedLNCC(torch.autograd.Function):
@@ -88,15 +92,18 @@ class _FusedLNCC(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, pred, target, kernel_size, smooth_dr, need_grad):
-        N, C = pred.shape[:2]
-        S = pred.shape[2:]
-        pf = pred.reshape(N * C, *S)
-        tf = target.reshape(N * C, *S)
         need = bool(need_grad and ctx.needs_input_grad[0])
-        traced = _traced(pf)
+        traced = _traced(pred)
         if traced:
+            # the registered op takes (B, D, H, W) volumes
+            N, C = pred.shape[:2]
+            S = pred.shape[2:]
+            pf = pred.reshape(N * C, *S)
+            tf = target.reshape(N * C, *S)
             loss, grad = torch.ops.fused_lncc.loss_grad(pf, tf, kernel_size, smooth_dr, need)
         else:
+            # the library reads (N, C, D, H, W) as N*C volumes; grad comes back in pred's shape
+            pf, tf = pred, target
             loss, grad = ext.loss_grad(pf, tf, kernel_size, smooth_dr, need)
         ctx.k = kernel_size
         ctx.dr = smooth_dr
@@ -115,21 +122,21 @@ class _FusedLNCC(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        saved = ctx.saved_tensors
-        pf, tf = saved[0], saved[1]
-        if len(saved) == 3:  # traced: functional form
-            g = saved[2] * grad_out.to(saved[2].dtype)
-            return g.reshape(ctx.shape), None, None, None, None
         g = ctx.grad
         ctx.grad = None
-        if ctx.traced:
+        if not ctx.traced:
             if g is None:  # second backward through a retained graph: recompute
-                _, g = torch.ops.fused_lncc.loss_grad(pf, tf, ctx.k, ctx.dr, True)
-            torch.ops.fused_lncc.scale_grad_(g, grad_out.detach())
-        else:
-            if g is None:
+                pf, tf = ctx.saved_tensors
                 _, g = ext.loss_grad(pf, tf, ctx.k, ctx.dr, True)
             ext.scale_grad_(g, grad_out)
+            return g, None, None, None, None
+        saved = ctx.saved_tensors
+        if len(saved) == 3:  # compiled: functional form
+            g = saved[2] * grad_out.to(saved[2].dtype)
+            return g.reshape(ctx.shape), None, None, None, None
+        if g is None:
+            _, g = torch.ops.fused_lncc.loss_grad(saved[0], saved[1], ctx.k, ctx.dr, True)
+        torch.ops.fused_lncc.scale_grad_(g, grad_out.detach())
         return g.reshape(ctx.shape), None, None, None, None
 
 

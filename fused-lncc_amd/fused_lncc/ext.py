@@ -29,7 +29,14 @@ def _check4d(name, t, like=None, dtype=None):
         raise RuntimeError(f"{name} must be {dtype}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(dev):
+    """Handle of the current stream of `dev` (torch's raw accessor skips building a Stream object,
+    ~2 us per call)."""
+    if _raw_stream is not None:
+        return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(dev).cuda_stream
 
 
@@ -56,6 +63,16 @@ class _on_device:
         return False
 
 
+def _check_vols(name, t, like=None, dtype=None):
+    """A contiguous (B, D, H, W) or (N, C, D, H, W) GPU tensor: volumes of the last three dims."""
+    if not (t.is_cuda and t.is_contiguous() and t.dim() in (4, 5)):
+        raise RuntimeError(f"{name} must be a contiguous 4D or 5D GPU tensor")
+    if like is not None and (t.shape != like.shape or t.device != like.device):
+        raise RuntimeError(f"{name} must match the shape and device of the other inputs")
+    if dtype is not None and t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {dtype}")
+
+
 def workspace_bytes(shape, kernel_size):
     B, D, H, W = shape
     return int(_lib.load().fl_workspace_bytes(B, D, H, W, int(kernel_size)))
@@ -63,12 +80,17 @@ def workspace_bytes(shape, kernel_size):
 
 def loss_grad(pf, tf, kernel_size, smooth_dr, need_grad=True):
     """Fused forward (+ gradient wrt pf, already multiplied by -1/M). Returns (loss, grad|None).
+    pf, tf: (B, D, H, W) or (N, C, D, H, W) with B = N*C volumes; grad has the shape of pf.
     Shape, k and dtype are validated by the C ABI before any device work."""
     code = _dtype_code(pf)
-    _check4d("pred", pf)
-    _check4d("target", tf, like=pf, dtype=pf.dtype)
+    _check_vols("pred", pf)
+    _check_vols("target", tf, like=pf, dtype=pf.dtype)
     lib = _lib.load()
-    B, D, H, W = pf.shape
+    if pf.dim() == 5:
+        N, C, D, H, W = pf.shape
+        B = N * C
+    else:
+        B, D, H, W = pf.shape
     k = int(kernel_size)
     with _on_device(pf.device):
         nbytes = lib.fl_workspace_bytes(B, D, H, W, k)

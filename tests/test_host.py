@@ -134,6 +134,31 @@ def test_fake_trace_of_loss_and_backward(dt):
     assert g_meta.dtype == dt and g_meta.shape == p.shape
 
 
+def test_traced_detection():
+    """Eager calls on plain tensors take the direct library path; under a dispatch-mode trace
+    (real-mode make_fx, a fake-tensor mode) or for a fake-tensor input the custom ops stand in."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    x = torch.ones(2, 3)
+    assert not fused_lncc._traced(x)
+    assert not fused_lncc._traced(torch.nn.Parameter(x))
+    seen = []
+
+    def f(a):
+        seen.append(fused_lncc._traced(a))
+        return a * 2
+
+    make_fx(f)(x)
+    make_fx(f, tracing_mode="fake")(x)
+    assert seen == [True, True]
+    mode = FakeTensorMode()
+    fx = mode.from_tensor(x)
+    assert fused_lncc._traced(fx)
+    with mode:
+        assert fused_lncc._traced(fx)
+
+
 def test_product_never_imports_the_oracle():
     pkg = os.path.dirname(fused_lncc.__file__)
     for fn in os.listdir(pkg):
