@@ -67,12 +67,21 @@ Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     return p;
 }
 
+// elem = bytes per element of the volumes; callers that do not know the dtype (workspace size,
+// finalize) pass the smallest, 2, and the launch that reads the volumes checks its own dtype.
 int check_shape(int64_t B, int64_t D, int64_t H, int64_t W, int elem) {
     if (B < 1 || D < 1 || H < 1 || W < 1) return fail(FL_E_SHAPE, "fused_lncc: empty volume (B, D, H, W must be >= 1)");
-    if (H * W * elem > kMaxPlaneBytes) return fail(FL_E_SHAPE, "fused_lncc: one (H, W) plane exceeds 2 GiB");
+    if (H > kMaxPlaneBytes || W > kMaxPlaneBytes || H * W * elem > kMaxPlaneBytes)
+        return fail(FL_E_SHAPE, "fused_lncc: one (H, W) plane exceeds 2 GiB");
     if (D > (1 << 30)) return fail(FL_E_SHAPE, "fused_lncc: D too large");
-    const int64_t tiles = B * ((W + fl::TX - 1) / fl::TX) * ((H + 23) / 24) * D;
-    if (tiles > 0x7fffffffLL) return fail(FL_E_SHAPE, "fused_lncc: too many volumes/tiles for one launch");
+    // workgroups of the largest launch plan (32 x 24 tiles, one per plane): a 31-bit grid,
+    // multiplied up factor by factor so that no product can overflow
+    int64_t tiles = B;
+    const int64_t factors[3] = {(W + fl::TX - 1) / fl::TX, (H + 23) / 24, D};
+    for (int64_t f : factors) {
+        if (tiles > 0x7fffffffLL / f) return fail(FL_E_SHAPE, "fused_lncc: too many volumes/tiles for one launch");
+        tiles *= f;
+    }
     return FL_OK;
 }
 
@@ -115,7 +124,7 @@ int fl_validate(int dtype, int kernel_size, int64_t B, int64_t D, int64_t H, int
 }
 
 size_t fl_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size) {
-    if (check_k(kernel_size) || check_shape(B, D, H, W, 4)) return 0;
+    if (check_k(kernel_size) || check_shape(B, D, H, W, 2)) return 0;
     return (size_t)plan_fused(B, D, H, W, kernel_size / 2).nblocks * sizeof(double);
 }
 
@@ -154,7 +163,8 @@ int fl_lncc_fused_partials(const void* pred, const void* target, int dtype, int6
 
 int fl_lncc_finalize(const void* workspace, int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size,
                      float* loss, void* stream) {
-    int rc = fl_validate(FL_F32, kernel_size, B, D, H, W);
+    int rc = check_k(kernel_size);
+    if (!rc) rc = check_shape(B, D, H, W, 2);
     if (rc) return rc;
     if (!workspace || !loss) return fail(FL_E_NULL, "fl_lncc_finalize: NULL pointer argument");
     const Plan p = plan_fused(B, D, H, W, kernel_size / 2);
@@ -240,6 +250,7 @@ int fl_lncc_backward(const float* A, const float* Bc, const float* Cc, const voi
     a.ntx = (int)((W + 15) / 16);
     a.nty = (int)((H + 15) / 16);
     a.scale = scale;
+    if (B * a.ntx * a.nty > 0x7fffffffLL) return fail(FL_E_SHAPE, "fl_lncc_backward: too many volumes/tiles for one launch");
     const uint32_t nb = (uint32_t)(B * a.ntx * a.nty);
     hipError_t e = fl::launch_box(kernel_size / 2, 3, dtype == FL_BF16, a, nb, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "fl_lncc_backward: launch");
@@ -259,6 +270,7 @@ int fl_box3d(const float* x, float* y, int64_t B, int64_t D, int64_t H, int64_t 
     a.ntx = (int)((W + 15) / 16);
     a.nty = (int)((H + 15) / 16);
     a.scale = 1.f;
+    if (B * a.ntx * a.nty > 0x7fffffffLL) return fail(FL_E_SHAPE, "fl_box3d: too many volumes/tiles for one launch");
     const uint32_t nb = (uint32_t)(B * a.ntx * a.nty);
     hipError_t e = fl::launch_box(kernel_size / 2, 1, false, a, nb, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "fl_box3d: launch");

@@ -79,6 +79,25 @@ def test_workspace_bytes():
     assert n > 0 and n % 8 == 0
     assert lib.fl_workspace_bytes(32, 128, 128, 128, 8) == 0
     assert ext.workspace_bytes((1, 1, 1, 1), 3) == 8
+    # a 30000 x 30000 plane is 1.8e9 B in bf16 (allowed) and 3.6e9 B in float32 (refused): the
+    # workspace size does not depend on the dtype, the launch checks its own
+    assert lib.fl_workspace_bytes(1, 8, 30000, 30000, 7) > 0
+    assert lib.fl_validate(_lib.FL_BF16, 7, 1, 8, 30000, 30000) == _lib.FL_OK
+    assert lib.fl_validate(_lib.FL_F32, 7, 1, 8, 30000, 30000) == _lib.FL_E_SHAPE
+
+
+def test_shape_limits_without_overflow():
+    lib = _lib.load()
+    # H*W*4 would overflow int64: refused by the per-dimension bound first
+    assert lib.fl_validate(_lib.FL_F32, 7, 1, 1, 2 ** 40, 2 ** 40) == _lib.FL_E_SHAPE
+    assert "2 GiB" in lib.fl_last_error().decode()
+    # B x tiles x D would overflow int64
+    assert lib.fl_validate(_lib.FL_F32, 7, 2 ** 62, 2 ** 30, 64, 64) == _lib.FL_E_SHAPE
+    assert "too many" in lib.fl_last_error().decode()
+    # the debug box-sum path has 16 x 16 tiles: a grid of 2^26 x 8 x 8 workgroups is refused on the
+    # host (nothing is launched)
+    assert lib.fl_box3d(8, 8, 2 ** 26, 1, 128, 128, 7, None) == _lib.FL_E_SHAPE
+    assert "too many" in lib.fl_last_error().decode()
 
 
 def test_python_api_errors():
