@@ -177,7 +177,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if dtname == "float32" else "bf16 (f32 accumulate)",
+        "dtype": "f32",  # the arithmetic type of the path; bf16 inputs are widened on load (config.input_dtype)
         "data": "synthetic",
         "config": {"workload": f"lncc fwd+bwd {a.workload}", "shape": list(spec["shape"]), "kernel_size": k,
                    "input_dtype": dtname, "bytes_per_voxel": BYTES_PER_VOXEL[dtname]},
