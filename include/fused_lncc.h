@@ -35,7 +35,8 @@ enum fl_status {
 /* Library version, (major << 16) | (minor << 8) | patch. */
 int fl_version(void);
 
-/* Message of the last failing call on this thread ("" if none). */
+/* Message of the last failing call on this thread ("" if none). The text is owned by the library
+ * and stays valid until the next failing call on the same thread: copy it to keep it. */
 const char* fl_last_error(void);
 
 /*
