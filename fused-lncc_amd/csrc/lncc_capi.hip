@@ -35,7 +35,7 @@ struct Plan {
 // workgroups (one workgroup per CU); FUSED_LNCC_DCHUNK overrides the chunk length for tuning.
 Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     Plan p;
-    const int ty = fl::tile_ty(halo);
+    const int ty = fl::TY;
     p.ntx = (int)((W + fl::TX - 1) / fl::TX);
     p.nty = (int)((H + ty - 1) / ty);
     const int64_t base = B * p.ntx * p.nty;
@@ -74,10 +74,10 @@ int check_shape(int64_t B, int64_t D, int64_t H, int64_t W, int elem) {
     if (H > kMaxPlaneBytes || W > kMaxPlaneBytes || H * W * elem > kMaxPlaneBytes)
         return fail(FL_E_SHAPE, "fused_lncc: one (H, W) plane exceeds 2 GiB");
     if (D > (1 << 30)) return fail(FL_E_SHAPE, "fused_lncc: D too large");
-    // workgroups of the largest launch plan (32 x 24 tiles, one per plane): a 31-bit grid,
+    // workgroups of the largest launch plan (32 x 32 tiles, one per plane): a 31-bit grid,
     // multiplied up factor by factor so that no product can overflow
     int64_t tiles = B;
-    const int64_t factors[3] = {(W + fl::TX - 1) / fl::TX, (H + 23) / 24, D};
+    const int64_t factors[3] = {(W + fl::TX - 1) / fl::TX, (H + fl::TY - 1) / fl::TY, D};
     for (int64_t f : factors) {
         if (tiles > 0x7fffffffLL / f) return fail(FL_E_SHAPE, "fused_lncc: too many volumes/tiles for one launch");
         tiles *= f;

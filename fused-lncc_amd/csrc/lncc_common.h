@@ -13,7 +13,7 @@ namespace fl {
 constexpr int NT = 1024;
 constexpr int WG_PER_CU = 1;
 constexpr int TX = 32;
-constexpr __host__ __device__ inline int tile_ty(int halo) { return halo == 4 ? 24 : 32; }
+constexpr int TY = 32;
 
 // gfx9 buffer resource word 3 (raw buffer, 32-bit data format); out-of-range loads return 0 and
 // out-of-range stores are dropped, which gives the zero padding of the box window for free.
@@ -124,7 +124,7 @@ constexpr int rup64(int n) { return (n + 63) / 64 * 64; }
 template <int H>
 struct Geo {
     static constexpr int K = 2 * H + 1;
-    static constexpr int TY = tile_ty(H);
+    static constexpr int TY = fl::TY;
     static constexpr int IX = TX + 4 * H, IY = TY + 4 * H;
     static constexpr int AX = TX + 2 * H, AY = TY + 2 * H;
     static constexpr int NIN = IX * IY;
