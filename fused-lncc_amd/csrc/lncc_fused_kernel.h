@@ -107,9 +107,12 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const int tid = threadIdx.x;
     const int D = a.dimD, Hd = a.dimH, Wd = a.dimW;
 
-    // workgroup -> tile; consecutive logical tiles (x-neighbours sharing halos) go to one XCD
+    // workgroup -> tile. Workgroups go to the 8 XCDs round-robin (workgroup i on XCD i % 8); XCD j
+    // takes the j-th contiguous range of logical tiles (q + (j < r) of them, q = nb / 8, r = nb % 8),
+    // so that neighbouring tiles, which share halo columns, share one L2
     const uint32_t nb = gridDim.x, bid = blockIdx.x;
-    uint32_t L = (nb % 8u == 0u) ? (bid % 8u) * (nb / 8u) + bid / 8u : bid;
+    const uint32_t xcd = bid % 8u, q8 = nb / 8u, r8 = nb % 8u;
+    uint32_t L = xcd * q8 + min(xcd, r8) + bid / 8u;
     const int tx = (int)(L % (uint32_t)a.ntx); L /= (uint32_t)a.ntx;
     const int ty = (int)(L % (uint32_t)a.nty); L /= (uint32_t)a.nty;
     const int tz = (int)(L % (uint32_t)a.nzc); L /= (uint32_t)a.nzc;
