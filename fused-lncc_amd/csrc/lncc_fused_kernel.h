@@ -371,13 +371,16 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     tnext[j] = load_elem<BF16>(rtn, voff[j]);
                 }
                 if constexpr (!RING) {
+                    // non-temporal: the last use of the halo columns' lines in this tile (the
+                    // central ones are re-read once more by AZ two steps later); marked evict-first
+                    // they leave the L2 to the planes that are still to be re-read
                     const bool okq = zi >= zq_lo && zi < zq_hi;
                     const __amdgpu_buffer_rsrc_t rpq = rsrc_at(pva + zoff - (K - 1) * PB, plane_bytes, okq);
                     const __amdgpu_buffer_rsrc_t rtq = rsrc_at(tva + zoff - (K - 1) * PB, plane_bytes, okq);
 #pragma unroll
                     for (int j = 0; j < J; ++j) {
-                        pold[j] = load_elem<BF16>(rpq, voff[j]);
-                        told[j] = load_elem<BF16>(rtq, voff[j]);
+                        pold[j] = load_elem<BF16, kNT>(rpq, voff[j]);
+                        told[j] = load_elem<BF16, kNT>(rtq, voff[j]);
                     }
                 }
             }
