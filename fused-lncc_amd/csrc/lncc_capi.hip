@@ -30,9 +30,10 @@ struct Plan {
     uint32_t nblocks;
 };
 
-// Workgroups: B volumes x (W/TX) x (H/TY) tiles x D-chunks. A chunk of d output planes costs d+4h
-// pipeline steps, so D is split only as far as needed to give the device at least two rounds of
-// workgroups (one workgroup per CU); FUSED_LNCC_DCHUNK overrides the chunk length for tuning.
+// Workgroups: B volumes x (W/TX) x (H/TY) tiles x D-chunks. A chunk of d output planes costs
+// d + 4h + 2 pipeline steps (it recomputes the halo planes of its neighbours), so D is split only
+// where that shortens the launch: small volumes, whose tiles alone leave CUs idle, get short chunks;
+// FUSED_LNCC_DCHUNK overrides the chunk length for tuning.
 Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     Plan p;
     const int ty = fl::TY;
@@ -43,11 +44,8 @@ Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     // workgroups run in rounds of one per CU (MI355X: 256 CUs): pick the split with the fewest
     // rounds x steps (ties: fewer workgroups).
     const int64_t kCUs = 256;
-    const int64_t minchunk = 4 * halo > 8 ? 4 * halo : 8;
-    int64_t maxz = D / minchunk;
-    if (maxz < 1) maxz = 1;
     int64_t best_cost = -1, dchunk = D;
-    for (int64_t nzc = 1; nzc <= maxz; ++nzc) {
+    for (int64_t nzc = 1; nzc <= D; ++nzc) {
         const int64_t d = (D + nzc - 1) / nzc;
         const int64_t blocks = base * ((D + d - 1) / d);
         const int64_t cost = ((blocks + kCUs - 1) / kCUs) * (d + 4 * halo + 2);
