@@ -227,6 +227,24 @@ def test_d_chunk_seams(k, dchunk, monkeypatch):
     assert_grad(g, gr)
 
 
+@pytest.mark.parametrize("shape,k,corr", [
+    ((1, 1, 100, 97, 131), 7, False),   # 240 workgroups: 20 partial tiles x 12 D-chunks of 9 planes
+    ((1, 1, 64, 200, 50), 9, True),     # 224 workgroups: 16 chunks of 4 planes, k = 9
+    ((2, 1, 70, 70, 70), 5, False),     # 252 workgroups (not a multiple of the 8 XCDs)
+    ((1, 3, 40, 65, 33), 3, True),      # 252 workgroups, 14 chunks of 3 planes
+])
+def test_medium_shapes_against_oracle(shape, k, corr):
+    """Volumes of about a million voxels, planned the way real launches are (short D-chunks for
+    small volumes, grids that are not multiples of 8, partial edge tiles), against the oracle."""
+    p, t = wl.randn_pair(shape, 70 + k)
+    if corr:  # high local correlation: ncc near 1, where the clamp and its masking matter
+        p = 0.9 * t + 0.1 * p
+    loss, g, _ = fused(p, t, k)
+    lr, gr = O.lncc(p.numpy(), t.numpy(), k)
+    assert_loss(loss, lr, LOSS_RTOL_F32)
+    assert_grad(g, gr)
+
+
 def test_unsupported_dtype_raises():
     p = torch.randn(1, 1, 16, 16, 16, device=DEV, dtype=torch.float64)
     with pytest.raises(RuntimeError):
