@@ -245,6 +245,26 @@ def test_medium_shapes_against_oracle(shape, k, corr):
     assert_grad(g, gr)
 
 
+def test_non_contiguous_inputs():
+    """Strided and transposed views are made contiguous by the API (fused_lncc/__init__.py:83 does
+    the same); the gradient reaches the original view through that copy."""
+    p, t = wl.randn_pair((1, 2, 20, 28, 24), 77)
+    base = p.transpose(3, 4).contiguous().to(DEV).requires_grad_(True)   # storage (.., 24, 28)
+    pv = base.transpose(3, 4)                                             # view (.., 28, 24)
+    tv = t.to(DEV)[..., :]
+    assert not pv.is_contiguous()
+    loss = fused_lncc_loss(pv, tv, 5)
+    loss.backward()
+    lr, gr = O.lncc(p.numpy(), t.numpy(), 5)
+    assert_loss(loss.item(), lr, LOSS_RTOL_F32)
+    assert_grad(base.grad.transpose(3, 4).double().cpu().numpy(), gr)
+    big = torch.randn(1, 2, 20, 28, 48, generator=torch.Generator().manual_seed(78))
+    ps, ts = big[..., ::2], big[..., 1::2]                                # strided slices
+    ls = fused_lncc_loss(ps.to(DEV), ts.to(DEV), 3)
+    lr2, _ = O.lncc(ps.contiguous().numpy(), ts.contiguous().numpy(), 3)
+    assert_loss(ls.item(), lr2, LOSS_RTOL_F32)
+
+
 def test_unsupported_dtype_raises():
     p = torch.randn(1, 1, 16, 16, 16, device=DEV, dtype=torch.float64)
     with pytest.raises(RuntimeError):
