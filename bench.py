@@ -37,6 +37,9 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--target-grad", action="store_true",
+                    help="time the step with the optional target-side gradient as well "
+                         "(fused_lncc_loss(..., target_grad=True)); 16 B/voxel fp32, 8 B/voxel bf16")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 268 MB device-to-device copy (calibrates HBM byte counters)")
     return ap.parse_args()
@@ -109,14 +112,15 @@ def main():
     p, t = wl.make_inputs(a.workload)
     dev = torch.device("cuda:0")
     p = p.to(dev).requires_grad_(True)
-    t = t.to(dev)
+    t = t.to(dev).requires_grad_(a.target_grad)
     dtname = str(p.dtype).replace("torch.", "")
     V = p.numel()
     torch.cuda.synchronize()
 
     def step():
         p.grad = None
-        fused_lncc_loss(p, t, k).backward()
+        t.grad = None
+        fused_lncc_loss(p, t, k, target_grad=a.target_grad).backward()
 
     for _ in range(a.warmup):
         step()
@@ -155,6 +159,9 @@ def main():
     kernel_ms = sum(kms) / len(kms)
     alg_bytes = V * BYTES_PER_VOXEL[dtname]
     achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
+    # the step's algorithmic bytes: with the target gradient, one more gradient is written
+    step_bpv = BYTES_PER_VOXEL[dtname] + (BYTES_PER_VOXEL[dtname] // 3 if a.target_grad else 0)
+    step_bytes = V * step_bpv
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -163,8 +170,10 @@ def main():
             traffic = prof.get("hbm_bytes_per_launch")
 
     out = {
-        "metric": METRIC if a.workload == "headline" else f"fwd+bwd GB/s, {a.workload} {spec['shape']} k={k}",
-        "value": round(alg_bytes / (ms_per_step * 1e-3) / 1e9, 3),
+        "metric": (METRIC if a.workload == "headline" and not a.target_grad else
+                   f"fwd+bwd{' (pred and target gradients)' if a.target_grad else ''} GB/s, "
+                   f"{a.workload} {spec['shape']} k={k}"),
+        "value": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 3),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": a.steps,
@@ -173,14 +182,14 @@ def main():
         "median_ms": round(median_ms, 5),
         "kernel_ms": round(kernel_ms, 5),
         "voxels_per_s": round(V / (ms_per_step * 1e-3), 1),
-        "pct_of_hbm_peak": round(100.0 * alg_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 3),
+        "pct_of_hbm_peak": round(100.0 * step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",  # the arithmetic type of the path; bf16 inputs are widened on load (config.input_dtype)
         "data": "synthetic",
         "config": {"workload": f"lncc fwd+bwd {a.workload}", "shape": list(spec["shape"]), "kernel_size": k,
-                   "input_dtype": dtname, "bytes_per_voxel": BYTES_PER_VOXEL[dtname]},
+                   "input_dtype": dtname, "bytes_per_voxel": step_bpv, "target_grad": a.target_grad},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
                      "kernel": "lncc_fused_kernel", "algorithmic_bytes_per_launch": alg_bytes},

@@ -88,12 +88,16 @@ def _traced(t):
 
 class _FusedLNCC(torch.autograd.Function):
     """Autograd wrapper: the gradient is produced in forward by the fused kernel and handed out in
-    backward (fused_lncc/__init__.py:49-74 computes it in backward from four saved fp32 maps)."""
+    backward (fused_lncc/__init__.py:49-74 computes it in backward from four saved fp32 maps).
+    The optional target-side gradient uses the symmetry of the loss in its two inputs: it is the
+    pred-side gradient of the same kernel with pred and target swapped."""
 
     @staticmethod
-    def forward(ctx, pred, target, kernel_size, smooth_dr, need_grad):
+    def forward(ctx, pred, target, kernel_size, smooth_dr, need_grad, need_tgrad):
         need = bool(need_grad and ctx.needs_input_grad[0])
+        need_t = bool(need_tgrad and ctx.needs_input_grad[1])
         traced = _traced(pred)
+        gt = None
         if traced:
             # the registered op takes (B, D, H, W) volumes
             N, C = pred.shape[:2]
@@ -101,56 +105,89 @@ class _FusedLNCC(torch.autograd.Function):
             pf = pred.reshape(N * C, *S)
             tf = target.reshape(N * C, *S)
             loss, grad = torch.ops.fused_lncc.loss_grad(pf, tf, kernel_size, smooth_dr, need)
+            if need_t:
+                _, gt = torch.ops.fused_lncc.loss_grad(tf, pf, kernel_size, smooth_dr, True)
         else:
             # the library reads (N, C, D, H, W) as N*C volumes; grad comes back in pred's shape
             pf, tf = pred, target
             loss, grad = ext.loss_grad(pf, tf, kernel_size, smooth_dr, need)
+            if need_t:
+                gt = ext.grad_only(tf, pf, kernel_size, smooth_dr)
         ctx.k = kernel_size
         ctx.dr = smooth_dr
         ctx.shape = pred.shape
         ctx.grad = None
+        ctx.tgrad = None
+        ctx.need = need
+        ctx.need_t = need_t
         ctx.traced = traced
-        if need:
+        if need or need_t:
             if _compiling():
-                ctx.save_for_backward(pf, tf, grad)
+                ctx.save_for_backward(pf, tf, grad if need else None, gt)
             else:
-                # kept outside save_for_backward so the first backward can scale it in place and
-                # hand it to AccumulateGrad without a copy
-                ctx.grad = grad
+                # kept outside save_for_backward so the first backward can scale them in place and
+                # hand them to AccumulateGrad without a copy
+                ctx.grad = grad if need else None
+                ctx.tgrad = gt
                 ctx.save_for_backward(pf, tf)
         return loss
 
     @staticmethod
     def backward(ctx, grad_out):
-        g = ctx.grad
+        g, gt = ctx.grad, ctx.tgrad
         ctx.grad = None
+        ctx.tgrad = None
         if not ctx.traced:
-            if g is None:  # second backward through a retained graph: recompute
+            if (ctx.need and g is None) or (ctx.need_t and gt is None):
+                # second backward through a retained graph: recompute
                 pf, tf = ctx.saved_tensors
-                _, g = ext.loss_grad(pf, tf, ctx.k, ctx.dr, True)
-            ext.scale_grad_(g, grad_out)
-            return g, None, None, None, None
+                if ctx.need and g is None:
+                    _, g = ext.loss_grad(pf, tf, ctx.k, ctx.dr, True)
+                if ctx.need_t and gt is None:
+                    gt = ext.grad_only(tf, pf, ctx.k, ctx.dr)
+            if g is not None:
+                ext.scale_grad_(g, grad_out)
+            if gt is not None:
+                ext.scale_grad_(gt, grad_out)
+            return g, gt, None, None, None, None
         saved = ctx.saved_tensors
-        if len(saved) == 3:  # compiled: functional form
-            g = saved[2] * grad_out.to(saved[2].dtype)
-            return g.reshape(ctx.shape), None, None, None, None
-        if g is None:
-            _, g = torch.ops.fused_lncc.loss_grad(saved[0], saved[1], ctx.k, ctx.dr, True)
-        torch.ops.fused_lncc.scale_grad_(g, grad_out.detach())
-        return g.reshape(ctx.shape), None, None, None, None
+        if len(saved) == 4:  # compiled: functional form
+            sg, sgt = saved[2], saved[3]
+            g = (sg * grad_out.to(sg.dtype)).reshape(ctx.shape) if ctx.need else None
+            gt = (sgt * grad_out.to(sgt.dtype)).reshape(ctx.shape) if ctx.need_t else None
+            return g, gt, None, None, None, None
+        pf, tf = saved
+        if ctx.need and g is None:
+            _, g = torch.ops.fused_lncc.loss_grad(pf, tf, ctx.k, ctx.dr, True)
+        if ctx.need_t and gt is None:
+            _, gt = torch.ops.fused_lncc.loss_grad(tf, pf, ctx.k, ctx.dr, True)
+        if g is not None:
+            torch.ops.fused_lncc.scale_grad_(g, grad_out.detach())
+            g = g.reshape(ctx.shape)
+        if gt is not None:
+            torch.ops.fused_lncc.scale_grad_(gt, grad_out.detach())
+            gt = gt.reshape(ctx.shape)
+        return g, gt, None, None, None, None
 
 
-def fused_lncc_loss(pred, target, kernel_size=7, smooth_dr=1e-5):
-    """1 - mean(squared local NCC) over all voxels. Gradient flows through ``pred`` only.
+def fused_lncc_loss(pred, target, kernel_size=7, smooth_dr=1e-5, *, target_grad=False):
+    """1 - mean(squared local NCC) over all voxels. Gradient flows through ``pred`` only, as in the
+    reference, unless ``target_grad=True``.
 
     pred, target: (N, C, D, H, W) float32 or bfloat16 ROCm tensors; kernel_size odd in 3..9.
-    Returns a 0-d float32 loss in [0, 1] (fused_lncc/__init__.py:77-83)."""
+    Returns a 0-d float32 loss in [0, 1] (fused_lncc/__init__.py:77-83).
+
+    target_grad (keyword only, not in the reference): also propagate the exact gradient to
+    ``target`` when it requires grad, as symmetric registration (both images warped) needs. It costs
+    a second pass of the fused kernel, with pred and target swapped."""
     assert pred.dim() == 5 and pred.shape == target.shape, "expect matching (N,C,D,H,W)"
     assert kernel_size % 2 == 1, "kernel_size must be odd"
     # The gradient is computed in the forward kernel only when autograd will ask for it; under
     # no_grad or for a pred without requires_grad the kernel reads 8 B/voxel and writes nothing.
-    need_grad = torch.is_grad_enabled() and pred.requires_grad
-    return _FusedLNCC.apply(pred.contiguous(), target.contiguous(), kernel_size, smooth_dr, need_grad)
+    grad_on = torch.is_grad_enabled()
+    need_grad = grad_on and pred.requires_grad
+    need_tgrad = bool(target_grad) and grad_on and target.requires_grad
+    return _FusedLNCC.apply(pred.contiguous(), target.contiguous(), kernel_size, smooth_dr, need_grad, need_tgrad)
 
 
 def lncc_map(pred, target, kernel_size=7, smooth_dr=1e-5):

@@ -106,6 +106,32 @@ def loss_grad(pf, tf, kernel_size, smooth_dr, need_grad=True):
     return loss, grad
 
 
+def grad_only(pf, tf, kernel_size, smooth_dr):
+    """The gradient of the loss with respect to pf alone (already multiplied by -1/M): the fused
+    kernel without the loss reduction. With pf and tf swapped it is the target-side gradient, the
+    loss being symmetric in its two inputs."""
+    code = _dtype_code(pf)
+    _check_vols("pred", pf)
+    _check_vols("target", tf, like=pf, dtype=pf.dtype)
+    lib = _lib.load()
+    if pf.dim() == 5:
+        N, C, D, H, W = pf.shape
+        B = N * C
+    else:
+        B, D, H, W = pf.shape
+    k = int(kernel_size)
+    with _on_device(pf.device):
+        nbytes = lib.fl_workspace_bytes(B, D, H, W, k)
+        if nbytes == 0:
+            _lib.check(lib.fl_validate(code, k, B, D, H, W))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=pf.device)
+        grad = torch.empty_like(pf)
+        _lib.check(lib.fl_lncc_fused_partials(
+            pf.data_ptr(), tf.data_ptr(), code, B, D, H, W, k, float(smooth_dr), grad.data_ptr(),
+            ws.data_ptr(), nbytes, _stream(pf.device)))
+    return grad
+
+
 def scale_grad_(grad, grad_out):
     """In place: grad *= grad_out (0-d float32 device tensor), skipped on the device when it is 1."""
     code = _dtype_code(grad)

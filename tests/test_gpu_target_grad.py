@@ -1,0 +1,83 @@
+"""The optional target-side gradient (fused_lncc_loss(..., target_grad=True)), outside the
+reference's own scope (its README.md:116-121: pred-only gradient) and what symmetric registration
+needs. Checked against the oracle's float64 PyTorch port, where autograd differentiates the loss
+with respect to target directly (not through the symmetry the kernel path uses)."""
+import pytest
+import torch
+
+import torch_lncc_port
+import workloads as wl
+from fused_lncc import fused_lncc_loss
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _ref_grads(p, t, k):
+    pr = p.double().requires_grad_(True)
+    tr = t.double().requires_grad_(True)
+    torch_lncc_port.lncc_dense(pr, tr, k).backward()
+    return pr.grad, tr.grad
+
+
+def _cos_rel(g, r):
+    g, r = g.double().cpu().ravel(), r.double().cpu().ravel()
+    return float(g @ r / (g.norm() * r.norm())), float((g - r).norm() / r.norm())
+
+
+@pytest.mark.parametrize("k", [3, 7, 9])
+def test_target_grad_matches_autograd(k):
+    p, t = wl.randn_pair((1, 2, 18, 21, 23), 90 + k)
+    p = 0.7 * t + 0.3 * p
+    gp_ref, gt_ref = _ref_grads(p, t, k)
+    pd = p.to(DEV).requires_grad_(True)
+    td = t.to(DEV).requires_grad_(True)
+    fused_lncc_loss(pd, td, k, target_grad=True).backward()
+    for g, r in ((pd.grad, gp_ref), (td.grad, gt_ref)):
+        c, rel = _cos_rel(g, r)
+        assert c > 0.9999 and rel < 1e-3, (c, rel)
+
+
+def test_default_is_pred_only_like_the_reference():
+    p, t = wl.randn_pair((1, 1, 12, 14, 16), 95)
+    pd = p.to(DEV).requires_grad_(True)
+    td = t.to(DEV).requires_grad_(True)
+    fused_lncc_loss(pd, td, 5).backward()
+    assert pd.grad is not None and td.grad is None
+
+
+def test_target_grad_alone_bf16_and_retained_graph():
+    p, t = wl.randn_pair((1, 2, 16, 20, 24), 96)
+    _, gt_ref = _ref_grads(p.bfloat16().float(), t.bfloat16().float(), 7)
+    pd = p.bfloat16().to(DEV)                       # pred without requires_grad
+    td = t.bfloat16().to(DEV).requires_grad_(True)
+    loss = fused_lncc_loss(pd, td, 7, target_grad=True)
+    (2.0 * loss).backward(retain_graph=True)
+    g1 = td.grad.clone()
+    td.grad = None
+    loss.backward()                                 # second backward through the retained graph
+    assert g1.dtype == torch.bfloat16 and pd.grad is None
+    c, rel = _cos_rel(g1.float(), 2.0 * gt_ref)
+    assert c > 0.999 and rel < 2e-2, (c, rel)
+    c, rel = _cos_rel(td.grad.float(), gt_ref)
+    assert c > 0.999 and rel < 2e-2, (c, rel)
+
+
+def test_target_grad_compiled_matches_eager():
+    torch._dynamo.reset()
+    p, t = wl.randn_pair((1, 2, 20, 24, 28), 97)
+
+    def step(a, b):
+        return fused_lncc_loss(a, b, 7, target_grad=True) + 0.1 * (a * b).mean()
+
+    def run(fn):
+        a = p.to(DEV).requires_grad_(True)
+        b = t.to(DEV).requires_grad_(True)
+        fn(a, b).backward()
+        torch.cuda.synchronize()
+        return a.grad, b.grad
+
+    ge = run(step)
+    gc = run(torch.compile(step, backend="aot_eager", fullgraph=True))
+    for x, y in zip(ge, gc):
+        assert torch.allclose(x, y, rtol=1e-6, atol=1e-6 * x.abs().max().item())

@@ -153,6 +153,26 @@ def test_fake_trace_of_loss_and_backward(dt):
     assert g_meta.dtype == dt and g_meta.shape == p.shape
 
 
+def test_fake_trace_with_target_grad():
+    """With target_grad=True the trace holds a second fused pass (inputs swapped) and both
+    gradients come out in the input dtype and shape."""
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    def step(p, t):
+        loss = fused_lncc_loss(p, t, 7, target_grad=True)
+        gp, gt = torch.autograd.grad(loss, (p, t))
+        return loss, gp, gt
+
+    p = torch.randn(1, 2, 8, 9, 10, dtype=torch.bfloat16, requires_grad=True)
+    t = torch.randn(1, 2, 8, 9, 10, dtype=torch.bfloat16, requires_grad=True)
+    gm = make_fx(step, tracing_mode="fake")(p, t)
+    calls = [n for n in gm.graph.nodes if n.op == "call_function" and "fused_lncc.loss_grad" in str(n.target)]
+    assert len(calls) == 2
+    outs = [n for n in gm.graph.nodes if n.op == "output"][0].args[0]
+    for o in outs[1:]:
+        assert o.meta["val"].dtype == torch.bfloat16 and o.meta["val"].shape == p.shape
+
+
 def test_traced_detection():
     """Eager calls on plain tensors take the direct library path; under a dispatch-mode trace
     (real-mode make_fx, a fake-tensor mode) or for a fake-tensor input the custom ops stand in."""
