@@ -186,6 +186,49 @@ int fl_lncc_loss_grad(const void* pred, const void* target, int dtype, int64_t B
     return fl_lncc_finalize(workspace, B, D, H, W, kernel_size, loss, stream);
 }
 
+int fl_lncc_loss_grad_pt(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,
+                         int64_t W, int kernel_size, float smooth_dr, float* loss, void* grad_pred,
+                         void* grad_target, void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = fl_validate(dtype, kernel_size, B, D, H, W);
+    if (rc) return rc;
+    if (!pred || !target || !loss || !grad_pred || !grad_target || !workspace)
+        return fail(FL_E_NULL, "fl_lncc_loss_grad_pt: NULL pointer argument");
+    const int halo = kernel_size / 2;
+    if (halo == 4) {
+        // five adjoint fields do not fit in LDS at k = 9: the pred pass, then the same kernel with
+        // pred and target swapped (the loss is symmetric); its partials are not reduced
+        rc = fl_lncc_loss_grad(pred, target, dtype, B, D, H, W, kernel_size, smooth_dr, loss, grad_pred, workspace,
+                               workspace_bytes, stream);
+        if (rc) return rc;
+        return fl_lncc_fused_partials(target, pred, dtype, B, D, H, W, kernel_size, smooth_dr, grad_target,
+                                      workspace, workspace_bytes, stream);
+    }
+    const Plan p = plan_fused(B, D, H, W, halo);
+    if (workspace_bytes < (size_t)p.nblocks * sizeof(double))
+        return fail(FL_E_WORKSPACE, "fl_lncc_loss_grad_pt: workspace needs " +
+                                        std::to_string((size_t)p.nblocks * sizeof(double)) + " bytes");
+    const double M = (double)B * (double)D * (double)H * (double)W;
+    fl::FusedArgs a = {};
+    a.pred = pred;
+    a.target = target;
+    a.grad = grad_pred;
+    a.tgrad = grad_target;
+    a.partials = static_cast<double*>(workspace);
+    a.dimD = (int)D;
+    a.dimH = (int)H;
+    a.dimW = (int)W;
+    a.ntx = p.ntx;
+    a.nty = p.nty;
+    a.nzc = p.nzc;
+    a.dchunk = p.dchunk;
+    a.inv_n = (float)(1.0 / ((double)kernel_size * kernel_size * kernel_size));
+    a.dr = smooth_dr;
+    a.gscale = (float)(2.0 / M);
+    hipError_t e = launch_fused(halo, fl::MODE_DUAL, dtype == FL_BF16, a, p.nblocks, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "fl_lncc_loss_grad_pt: fused kernel launch");
+    return fl_lncc_finalize(workspace, B, D, H, W, kernel_size, loss, stream);
+}
+
 int fl_scale_grad(void* grad, int dtype, int64_t n, const float* grad_out, void* stream) {
     int rc = check_dtype(dtype);
     if (rc) return rc;

@@ -121,7 +121,9 @@ constexpr int rup64(int n) { return (n + 63) / 64 * 64; }
 // output range up to whole segments: the extra outputs read row padding and land in padding rows
 // of the destination that no later pass reads (and that the loss never counts), so no lane needs
 // a per-output store mask.
-template <int H>
+// NA = number of adjoint fields carried from Y to AZ: 3 (alpha, beta, gamma of the pred gradient)
+// or 5 (with alpha', beta' of the target gradient; gamma is shared)
+template <int H, int NA = 3>
 struct Geo {
     static constexpr int K = 2 * H + 1;
     static constexpr int TY = fl::TY;
@@ -144,15 +146,17 @@ struct Geo {
     // fill the first waves and the AX units (3 per item) start on the next wave boundary; in
     // phase P0 the Y items fill the first waves (SIMDs 0 and 1 get the extra ones) and the AYs
     // units (3 per item) go to waves 10, 11, 14, 15 (SIMDs 2 and 3), B_PER_WAVE each.
-    static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, AX_LANE0 = rup64(UX), U1 = 1;
-    static constexpr int UB = 3 * BITEMS, B_PER_WAVE = UB / 4;
-    static_assert(YITEMS <= 10 * 64 && AX_LANE0 + UA <= NT && UB == 192 && B_PER_WAVE == 48 && BSEG == 2 && TX == 32,
+    // With five adjoint fields the AYs units (two rows of 32 per field) take five whole waves.
+    static constexpr int UX = 5 * XITEMS, UA = NA * AITEMS, AX_LANE0 = rup64(UX), U1 = 1;
+    static constexpr int UB = NA * BITEMS, B_PER_WAVE = NA == 3 ? UB / 4 : 64;
+    static_assert(YITEMS <= 10 * 64 && AX_LANE0 + UA <= NT && BSEG == 2 && TX == 32 &&
+                      (NA == 3 ? (UB == 192 && B_PER_WAVE == 48) : (NA == 5 && UB == 320)),
                   "lanes");
     // every segment starts on a 16-byte boundary (rows are read as float4)
     static_assert(XR >= AX && TX % SA == 0 && TY % SB == 0 && SX % 4 == 0 && SY % 4 == 0 &&
                       SA % 4 == 0 && SB % 4 == 0, "segments");
-    // LDS layout (floats): Zs[5][IY][ZS], XsT[5][XR][XS] (transposed), Gs[3][YR][GS],
-    // GXsT[3][TX][GXS] (transposed), GY[3][TY][GYS]; each buffer but GY ends in PAD spare floats
+    // LDS layout (floats): Zs[5][IY][ZS], XsT[5][XR][XS] (transposed), Gs[NA][YR][GS],
+    // GXsT[NA][TX][GXS] (transposed), GY[NA][TY][GYS]; each buffer but GY ends in PAD spare floats
     static constexpr int ZS = stride4(IX), XS = stride4(cmax(IY, AY)), GS = stride4(AX), GXS = XS;
     static constexpr int GYS = TX + 1, PAD = 16;
     static constexpr int ZP = IY * ZS, XP = XR * XS, GP = YR * GS, GXP = TX * GXS, GYP = TY * GYS;
@@ -161,7 +165,7 @@ struct Geo {
     static_assert(SX + rup4(SX + 2 * H) <= ZS + PAD && YR - SY + rup4(SY + 2 * H) <= XS + PAD &&
                       TX - SA + rup4(SA + 2 * H) <= GS + PAD && TY - SB + rup4(SB + 2 * H) <= GXS + PAD,
                   "row reads");
-    static constexpr int LDS_FLOATS = 5 * (ZP + XP) + 3 * (GP + GXP + GYP) + 4 * PAD;
+    static constexpr int LDS_FLOATS = 5 * (ZP + XP) + NA * (GP + GXP + GYP) + 4 * PAD;
     static_assert(LDS_FLOATS * 4 <= 160 * 1024, "LDS");
 };
 

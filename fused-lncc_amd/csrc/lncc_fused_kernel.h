@@ -23,6 +23,10 @@
 // plane, P0 = {F(zi), Y(zi-1), AYs(zi-2)} and P1 = {X(zi), AX(zi-1), AZ(zi-2)}, so each plane costs
 // two workgroup barriers, and the stages that share a phase run on disjoint waves.
 //
+// MODE_DUAL adds the gradient with respect to target (not in the reference): the loss is symmetric
+// in p and t, so Y also forms alpha and beta with the roles of p and t swapped, and AX, AYs and AZ
+// carry five fields (gamma is shared).
+//
 // Reference semantics (fused_lncc/csrc/lncc3d.cu:93-107, baselines/torch_lncc.py:25-32):
 //   cross = Spt - Sp St/n ; vp = max(Spp - Sp^2/n, 0) + dr ; vt likewise ; ncc = cross^2/(vp vt);
 //   ncc >= 1 -> ncc = 1 and zero adjoints; NaN keeps NaN ncc and zero adjoints;
@@ -88,9 +92,13 @@ __device__ __forceinline__ void window_sums(const float (&v)[S + 2 * H], float (
 
 template <int HH, bool BF16, int MODE>
 __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) {
-    using G = Geo<HH>;
+    // DUAL: the target gradient too, from two more adjoint fields (the loss is symmetric in p and
+    // t, so they are alpha and beta with the roles of p and t swapped; gamma is shared)
+    constexpr bool DUAL = (MODE == MODE_DUAL);
+    constexpr bool ADJ = (MODE == MODE_GRAD) || DUAL;
+    constexpr int NA = DUAL ? 5 : 3;
+    using G = Geo<HH, NA>;
     constexpr int K = G::K;
-    constexpr bool ADJ = (MODE == MODE_GRAD);
     constexpr int ELEM = BF16 ? 2 : 4;
     constexpr int J = G::J;
     constexpr int TY = G::TY;
@@ -99,9 +107,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // alias the writes of another and can overlap them
     __shared__ __align__(16) float Zs[5 * G::ZP + G::PAD];
     __shared__ __align__(16) float Xs[5 * G::XP + G::PAD];
-    __shared__ __align__(16) float Gs[ADJ ? 3 * G::GP + G::PAD : 4];
-    __shared__ __align__(16) float GXs[ADJ ? 3 * G::GXP + G::PAD : 4];
-    __shared__ __align__(16) float GY[ADJ ? 3 * G::GYP : 2];
+    __shared__ __align__(16) float Gs[ADJ ? NA * G::GP + G::PAD : 4];
+    __shared__ __align__(16) float GXs[ADJ ? NA * G::GXP + G::PAD : 4];
+    __shared__ __align__(16) float GY[ADJ ? NA * G::GYP : 2];
     __shared__ double red[NT / 64];
 
     const int tid = threadIdx.x;
@@ -124,6 +132,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const char* pvol = (const char*)a.pred + b * D * HW * ELEM;
     const char* tvol = (const char*)a.target + b * D * HW * ELEM;
     char* const gvol = ADJ ? (char*)a.grad + b * D * HW * ELEM : nullptr;
+    char* const tgvol = DUAL ? (char*)a.tgrad + b * D * HW * ELEM : nullptr;
 
     // ---- F: per-lane input columns
     uint32_t voff[J];
@@ -158,14 +167,14 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             u_dst[k] = q * G::XP + start * G::XS + iy;
         } else if (ADJ && u >= G::AX_LANE0 && u < G::AX_LANE0 + G::UA) {
             int row, ay;  // rows (c, seg) of AY positions
-            split32<G::AY>(u - G::AX_LANE0, 3 * G::ASEG, row, ay);
+            split32<G::AY>(u - G::AX_LANE0, NA * G::ASEG, row, ay);
             const int c = row / G::ASEG, start = (row % G::ASEG) * G::SA;
             u_kind[k] = 2;
             u_src[k] = c * G::GP + ay * G::GS + start;
             u_dst[k] = c * G::GXP + start * G::GXS + ay;
         }
     }
-    // P0: Y items on lanes [0, YITEMS), AYs units on waves 10, 11, 14, 15
+    // P0: Y items on lanes [0, YITEMS), AYs units on waves 10, 11, 14, 15 (and 6 with five fields)
     const bool has_y = tid < G::YITEMS;
     int y_seg = 0, y_ax = 0;  // rows seg of AX positions
     if (has_y) split32<G::AX>(tid, G::YSEG, y_seg, y_ax);
@@ -184,15 +193,23 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             y_core[i] = y_inv[i] && corex && ay >= HH && ay < HH + TY;
         }
     }
-    const int wave = tid >> 6, bslot = wave == 10 ? 0 : wave == 11 ? 1 : wave == 14 ? 2 : wave == 15 ? 3 : -1;
+    const int wave = tid >> 6;
+    const int bslot = wave == 10 ? 0 : wave == 11 ? 1 : wave == 14 ? 2 : wave == 15 ? 3 : (DUAL && wave == 6) ? 4 : -1;
     const bool has_b = ADJ && bslot >= 0 && (tid & 63) < G::B_PER_WAVE;
     int b_src = 0, b_dst = 0;
     if (has_b) {
-        // rows (c, seg) of TX = 32 positions: slot s takes row s on its first 32 lanes and half
-        // of row 4 + s/2 on the next 16
+        // rows (c, seg) of TX = 32 positions. Three fields: slot s takes row s on its first 32
+        // lanes and half of row 4 + s/2 on the next 16. Five fields: slot s takes both rows of
+        // field s (32 lanes each).
         const int l = tid & 63;
-        const int row = l < 32 ? bslot : 4 + (bslot >> 1);
-        const int ox = l < 32 ? l : (bslot & 1) * 16 + (l - 32);
+        int row, ox;
+        if constexpr (DUAL) {
+            row = 2 * bslot + (l >> 5);
+            ox = l & 31;
+        } else {
+            row = l < 32 ? bslot : 4 + (bslot >> 1);
+            ox = l < 32 ? l : (bslot & 1) * 16 + (l - 32);
+        }
         const int c = row / G::BSEG, start = (row % G::BSEG) * G::SB;
         b_src = c * G::GXP + ox * G::GXS + start;
         b_dst = c * G::GYP + start * G::GYS + ox;
@@ -212,7 +229,8 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // the window comes from a k-deep register ring of the last k planes' p,t (k <= 7) or, where
     // the ring would not fit in the register budget (k = 9), is re-read from global memory (still
     // cache resident) and prefetched like the new plane
-    constexpr bool RING = K <= 7;
+    // (the five-field mode spends those registers on its two extra z-rings of xy-sums instead)
+    constexpr bool RING = K <= 7 && !DUAL;
     constexpr int KR = RING ? K : 1;
     float zsum[J][5], pnext[J], tnext[J], pring[KR][J], tring[KR][J], pold[J], told[J];
     float pz = 0.f, tzz = 0.f;  // AZ: p,t at this step's output plane (prefetched one step ahead)
@@ -237,9 +255,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             tnext[j] = load_elem<BF16>(rt, voff[j]);
         }
     }
-    float gring[3][K], gz[3];
+    float gring[NA][K], gz[NA];
 #pragma unroll
-    for (int c = 0; c < 3; ++c) {
+    for (int c = 0; c < NA; ++c) {
         gz[c] = 0.f;
 #pragma unroll
         for (int r = 0; r < K; ++r) gring[c][r] = 0.f;
@@ -253,7 +271,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // zero-sized resource (its address is never dereferenced).
     const uint64_t PB = (uint64_t)HW * ELEM;
     const uint64_t pva = (uint64_t)(uintptr_t)pvol, tva = (uint64_t)(uintptr_t)tvol;
-    const uint64_t gva = (uint64_t)(uintptr_t)gvol;
+    const uint64_t gva = (uint64_t)(uintptr_t)gvol, tgva = (uint64_t)(uintptr_t)tgvol;
     uint64_t zoff = (uint64_t)zlo * PB;
     const int zn_hi = min(zhi, D);                 // F: new plane zi+1 valid while zi+1 < zn_hi
     const int zq_lo = zlo + K - 1, zq_hi = min(D + K - 1, zhi - 1);  // old plane zi+1-K: zi in [zq_lo, zq_hi)
@@ -301,6 +319,12 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                         Gs[0 * G::GP + ay * G::GS + y_ax] = crm * w;
                         Gs[1 * G::GP + ay * G::GS + y_ax] = crm * uu;
                         Gs[2 * G::GP + ay * G::GS + y_ax] = crm;
+                        if constexpr (DUAL) {  // the same with p and t swapped
+                            const float ut = crm * vp;
+                            const float wt = fmaf(-St, ut, Sp);
+                            Gs[3 * G::GP + ay * G::GS + y_ax] = crm * wt;
+                            Gs[4 * G::GP + ay * G::GS + y_ax] = crm * ut;
+                        }
                     }
                     if constexpr (MODE == MODE_MAPS) {
                         if (count && y_core[i]) {
@@ -411,11 +435,11 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 // AZ(zi-2): z ring of the xy-sums, combine at the output plane zo (lanes without an
                 // output column run on a clamped one and store out of range, i.e. nothing)
                 {
-                    float ys[3];
+                    float ys[NA];
 #pragma unroll
-                    for (int c = 0; c < 3; ++c) ys[c] = actB ? GY[c * G::GYP + z_oy * G::GYS + z_ox] : 0.f;
+                    for (int c = 0; c < NA; ++c) ys[c] = actB ? GY[c * G::GYP + z_oy * G::GYS + z_ox] : 0.f;
 #pragma unroll
-                    for (int c = 0; c < 3; ++c) {
+                    for (int c = 0; c < NA; ++c) {
                         gz[c] += ys[c] - gring[c][r];
                         gring[c][r] = ys[c];
                     }
@@ -430,6 +454,10 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     // half): those stores keep the default policy, so that the L2 merges the two
                     // halves into one write.
                     store_elem_buf<BF16, BF16 ? 0 : kNT>(rsrc_at(gva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, g);
+                    if constexpr (DUAL) {
+                        const float gt = a.gscale * fmaf(inv_n, gz[3], fmaf(tzz, gz[4], -pz * gz[2]));
+                        store_elem_buf<BF16, BF16 ? 0 : kNT>(rsrc_at(tgva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, gt);
+                    }
                     // prefetch p,t at the next step's output plane; issued after this step's use, so
                     // one register each suffices and no copy has to wait for the load
                     const bool oko = zo + 1 >= z0 && zo + 1 < z1;
@@ -464,8 +492,17 @@ hipError_t launch_fused(int mode, bool bf16, const FusedArgs& a, uint32_t nblock
         if (bf16) FL_LAUNCH(true, MODE_LOSS); else FL_LAUNCH(false, MODE_LOSS);
     } else if (mode == MODE_GRAD) {
         if (bf16) FL_LAUNCH(true, MODE_GRAD); else FL_LAUNCH(false, MODE_GRAD);
-    } else {
+    } else if (mode == MODE_MAPS) {
         if (bf16) FL_LAUNCH(true, MODE_MAPS); else FL_LAUNCH(false, MODE_MAPS);
+    } else if (mode == MODE_DUAL) {
+        // five adjoint fields fit in LDS for k <= 7 only; k = 9 takes two MODE_GRAD passes
+        if constexpr (HH <= 3) {
+            if (bf16) FL_LAUNCH(true, MODE_DUAL); else FL_LAUNCH(false, MODE_DUAL);
+        } else {
+            return hipErrorInvalidValue;
+        }
+    } else {
+        return hipErrorInvalidValue;
     }
 #undef FL_LAUNCH
     return hipGetLastError();

@@ -5,12 +5,14 @@
 
 namespace fl {
 
-enum Mode { MODE_LOSS = 0, MODE_GRAD = 1, MODE_MAPS = 2 };
+// MODE_DUAL: the gradients with respect to pred and to target in one pass (k <= 7)
+enum Mode { MODE_LOSS = 0, MODE_GRAD = 1, MODE_MAPS = 2, MODE_DUAL = 3 };
 
 struct FusedArgs {
     const void* pred;
     const void* target;
-    void* grad;       // MODE_GRAD: gradient wrt pred, pred dtype
+    void* grad;       // MODE_GRAD, MODE_DUAL: gradient wrt pred, pred dtype
+    void* tgrad;      // MODE_DUAL: gradient wrt target, target dtype
     float* ncc_map;   // MODE_MAPS: fp32 maps ncc, A, Bc, Cc (reference definitions)
     float* a_map;
     float* b_map;

@@ -110,9 +110,12 @@ class _FusedLNCC(torch.autograd.Function):
         else:
             # the library reads (N, C, D, H, W) as N*C volumes; grad comes back in pred's shape
             pf, tf = pred, target
-            loss, grad = ext.loss_grad(pf, tf, kernel_size, smooth_dr, need)
-            if need_t:
-                gt = ext.grad_only(tf, pf, kernel_size, smooth_dr)
+            if need and need_t:  # one pass for both gradients
+                loss, grad, gt = ext.loss_grad_pt(pf, tf, kernel_size, smooth_dr)
+            else:
+                loss, grad = ext.loss_grad(pf, tf, kernel_size, smooth_dr, need)
+                if need_t:
+                    gt = ext.grad_only(tf, pf, kernel_size, smooth_dr)
         ctx.k = kernel_size
         ctx.dr = smooth_dr
         ctx.shape = pred.shape
@@ -141,9 +144,11 @@ class _FusedLNCC(torch.autograd.Function):
             if (ctx.need and g is None) or (ctx.need_t and gt is None):
                 # second backward through a retained graph: recompute
                 pf, tf = ctx.saved_tensors
-                if ctx.need and g is None:
+                if ctx.need and ctx.need_t:
+                    _, g, gt = ext.loss_grad_pt(pf, tf, ctx.k, ctx.dr)
+                elif ctx.need:
                     _, g = ext.loss_grad(pf, tf, ctx.k, ctx.dr, True)
-                if ctx.need_t and gt is None:
+                else:
                     gt = ext.grad_only(tf, pf, ctx.k, ctx.dr)
             if g is not None:
                 ext.scale_grad_(g, grad_out)

@@ -106,6 +106,33 @@ def loss_grad(pf, tf, kernel_size, smooth_dr, need_grad=True):
     return loss, grad
 
 
+def loss_grad_pt(pf, tf, kernel_size, smooth_dr):
+    """The loss and both gradients (wrt pf and wrt tf, each already multiplied by -1/M) from one
+    fused pass (k <= 7; two passes at k = 9). Returns (loss, grad_pred, grad_target)."""
+    code = _dtype_code(pf)
+    _check_vols("pred", pf)
+    _check_vols("target", tf, like=pf, dtype=pf.dtype)
+    lib = _lib.load()
+    if pf.dim() == 5:
+        N, C, D, H, W = pf.shape
+        B = N * C
+    else:
+        B, D, H, W = pf.shape
+    k = int(kernel_size)
+    with _on_device(pf.device):
+        nbytes = lib.fl_workspace_bytes(B, D, H, W, k)
+        if nbytes == 0:
+            _lib.check(lib.fl_validate(code, k, B, D, H, W))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=pf.device)
+        loss = torch.empty((), dtype=torch.float32, device=pf.device)
+        gp = torch.empty_like(pf)
+        gt = torch.empty_like(tf)
+        _lib.check(lib.fl_lncc_loss_grad_pt(
+            pf.data_ptr(), tf.data_ptr(), code, B, D, H, W, k, float(smooth_dr), loss.data_ptr(), gp.data_ptr(),
+            gt.data_ptr(), ws.data_ptr(), nbytes, _stream(pf.device)))
+    return loss, gp, gt
+
+
 def grad_only(pf, tf, kernel_size, smooth_dr):
     """The gradient of the loss with respect to pf alone (already multiplied by -1/M): the fused
     kernel without the loss reduction. With pf and tf swapped it is the target-side gradient, the

@@ -76,6 +76,19 @@ int fl_lncc_finalize(const void* workspace, int64_t B, int64_t D, int64_t H, int
                      float* loss, void* stream);
 
 /*
+ * Both gradients: *loss as fl_lncc_loss_grad, grad_pred = d loss / d pred and grad_target =
+ * d loss / d target (each in the input dtype, already multiplied by -1/M), all required. No
+ * counterpart in the reference, whose gradient goes to pred only (its README.md:116-121); it is
+ * the target-side gradient that FireANTs computes for symmetric registration. The loss is symmetric
+ * in its two inputs, so the target gradient is the pred gradient with the two swapped: for k <= 7
+ * one fused kernel carries both (five adjoint fields instead of three), for k = 9 it runs as two
+ * passes of the pred-gradient kernel. Same workspace as fl_lncc_loss_grad.
+ */
+int fl_lncc_loss_grad_pt(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,
+                         int64_t W, int kernel_size, float smooth_dr, float* loss, void* grad_pred,
+                         void* grad_target, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * grad *= *grad_out (device scalar), done on the device and skipped there when *grad_out == 1, so
  * the common loss.backward() path costs one tiny launch and no host sync. Replaces the tensor
  * multiply by -grad_out/M of _FusedLNCC.backward, fused_lncc/__init__.py:73.

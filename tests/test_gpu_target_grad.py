@@ -81,3 +81,29 @@ def test_target_grad_compiled_matches_eager():
     gc = run(torch.compile(step, backend="aot_eager", fullgraph=True))
     for x, y in zip(ge, gc):
         assert torch.allclose(x, y, rtol=1e-6, atol=1e-6 * x.abs().max().item())
+
+
+@pytest.mark.parametrize("k", [3, 5, 7, 9])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dchunk", [None, 3])
+def test_dual_kernel_against_single_passes(k, dt, dchunk, monkeypatch):
+    """The one-pass kernel for both gradients (k <= 7; two passes at k = 9) gives the pred
+    gradient of the pred-only kernel bit for bit (same sums in the same order) and the target
+    gradient of that kernel run with the inputs swapped, on a ragged shape with D-chunk seams."""
+    from fused_lncc import ext
+
+    if dchunk is not None:
+        monkeypatch.setenv("FUSED_LNCC_DCHUNK", str(dchunk))
+    p, t = wl.randn_pair((2, 1, 19, 37, 45), 120 + k)
+    pf = p.reshape(2, 19, 37, 45).to(dt).to(DEV)
+    tf = t.reshape(2, 19, 37, 45).to(dt).to(DEV)
+    loss, gp, gt = ext.loss_grad_pt(pf, tf, k, 1e-5)
+    loss1, gp1 = ext.loss_grad(pf, tf, k, 1e-5, True)
+    gt1 = ext.grad_only(tf, pf, k, 1e-5)
+    torch.cuda.synchronize()
+    assert gp.dtype == dt and gt.dtype == dt
+    assert torch.equal(gp, gp1)
+    assert loss.item() == loss1.item()
+    tol = 1e-6 if dt == torch.float32 else 1e-2
+    c, rel = _cos_rel(gt.float(), gt1.float())
+    assert c > 1 - tol and rel < 10 * tol, (c, rel)
