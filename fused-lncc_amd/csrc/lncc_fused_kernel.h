@@ -6,9 +6,9 @@
 //
 //   F   (registers) lanes own the input columns of the (TX+4h) x (TY+4h) region and keep running
 //       z-sums of p, t, p^2, t^2, p*t: add plane zi (prefetched one plane ahead), subtract plane
-//       zi-k (from a k-deep register ring of p,t; for k = 9, where the ring does not fit the
-//       register budget, re-read from global memory, still cache resident, and prefetched too);
-//       write the five z-sums to LDS.
+//       zi-k (from a k-deep register ring of p,t; for k = 9 and in MODE_DUAL, where the ring does
+//       not fit the register budget, re-read from global memory, still cache resident, and
+//       prefetched too); write the five z-sums to LDS.
 //   X   running x-sums of the five z-sums over the (TX+2h)-wide adjoint range.
 //   Y   running y-sums -> the five k^3 box-sums on the (TX+2h) x (TY+2h) adjoint region; per voxel
 //       squared NCC (clamped to 1), loss partial sums, and the adjoint coefficients alpha, beta,
@@ -227,9 +227,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 
     // F state: running z-sums; p,t of the next plane (prefetched one step ahead); the plane leaving
     // the window comes from a k-deep register ring of the last k planes' p,t (k <= 7) or, where
-    // the ring would not fit in the register budget (k = 9), is re-read from global memory (still
-    // cache resident) and prefetched like the new plane
-    // (the five-field mode spends those registers on its two extra z-rings of xy-sums instead)
+    // the ring would not fit in the register budget, is re-read from global memory (still cache
+    // resident) and prefetched like the new plane: at k = 9, and in the five-field mode, which
+    // spends those registers on its two extra z-rings of xy-sums
     constexpr bool RING = K <= 7 && !DUAL;
     constexpr int KR = RING ? K : 1;
     float zsum[J][5], pnext[J], tnext[J], pring[KR][J], tring[KR][J], pold[J], told[J];
