@@ -121,6 +121,20 @@ int fl_validate(int dtype, int kernel_size, int64_t B, int64_t D, int64_t H, int
     return check_shape(B, D, H, W, dtype == FL_BF16 ? 2 : 4);
 }
 
+size_t fl_lds_bytes(int kernel_size, int dtype) {
+    if (check_k(kernel_size) || check_dtype(dtype)) return 0;
+    // the static LDS of the gradient kernel: the five z-sum and x-sum planes, the three adjoint
+    // planes at each pass, and the per-wave partials of the loss (the same for both dtypes)
+    size_t floats = 0;
+    switch (kernel_size / 2) {
+        case 1: floats = fl::Geo<1>::LDS_FLOATS; break;
+        case 2: floats = fl::Geo<2>::LDS_FLOATS; break;
+        case 3: floats = fl::Geo<3>::LDS_FLOATS; break;
+        default: floats = fl::Geo<4>::LDS_FLOATS; break;
+    }
+    return floats * sizeof(float) + (fl::NT / 64) * sizeof(double);
+}
+
 size_t fl_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size) {
     if (check_k(kernel_size) || check_shape(B, D, H, W, 2)) return 0;
     return (size_t)plan_fused(B, D, H, W, kernel_size / 2).nblocks * sizeof(double);

@@ -29,6 +29,7 @@ SIGNATURES = {
     "fl_last_error": (ctypes.c_char_p, []),
     "fl_validate": (_I, [_I, _I, _L, _L, _L, _L]),
     "fl_workspace_bytes": (_S, [_L, _L, _L, _L, _I]),
+    "fl_lds_bytes": (_S, [_I, _I]),
     "fl_lncc_loss_grad": (_I, [_P, _P, _I, _L, _L, _L, _L, _I, _F, _P, _P, _P, _S, _P]),
     "fl_lncc_fused_partials": (_I, [_P, _P, _I, _L, _L, _L, _L, _I, _F, _P, _P, _S, _P]),
     "fl_lncc_loss_grad_pt": (_I, [_P, _P, _I, _L, _L, _L, _L, _I, _F, _P, _P, _P, _P, _S, _P]),

@@ -46,6 +46,14 @@ const char* fl_last_error(void);
  */
 int fl_validate(int dtype, int kernel_size, int64_t B, int64_t D, int64_t H, int64_t W);
 
+/*
+ * Bytes of LDS one workgroup of the gradient kernel uses for this kernel size (static; 0 for an
+ * invalid k or dtype), for callers that check a device's limit before launching. Replaces the
+ * per-call shared-memory cap check of lncc_forward / lncc_backward, fused_lncc/csrc/lncc3d.cu:144-147,
+ * 268-270 (MI355X: 160 KB per workgroup; every kernel size fits).
+ */
+size_t fl_lds_bytes(int kernel_size, int dtype);
+
 /* Device bytes of the workspace fl_lncc_loss_grad needs for this shape (per-workgroup partials). */
 size_t fl_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size);
 

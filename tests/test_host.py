@@ -86,6 +86,14 @@ def test_workspace_bytes():
     assert lib.fl_validate(_lib.FL_F32, 7, 1, 8, 30000, 30000) == _lib.FL_E_SHAPE
 
 
+def test_lds_bytes():
+    lib = _lib.load()
+    sizes = [lib.fl_lds_bytes(k, _lib.FL_F32) for k in (3, 5, 7, 9)]
+    assert all(0 < b <= 160 * 1024 for b in sizes) and sizes == sorted(sizes)
+    assert lib.fl_lds_bytes(7, _lib.FL_BF16) == sizes[2]
+    assert lib.fl_lds_bytes(8, _lib.FL_F32) == 0 and lib.fl_lds_bytes(7, 5) == 0
+
+
 def test_shape_limits_without_overflow():
     lib = _lib.load()
     # H*W*4 would overflow int64: refused by the per-dimension bound first
