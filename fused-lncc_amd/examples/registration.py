@@ -6,7 +6,7 @@ The consumer of the loss that the reference demonstrates end to end
 The warp is trilinear ``grid_sample``; the regularizer is the mean squared finite difference of
 the field along each axis. Nothing here is specific to the GPU beyond the loss.
 
-    python fused-lncc_amd/examples/registration.py --size 96 --iters 150
+    python fused-lncc_amd/examples/registration.py --size 96 --iters 150 [--graph]
 
 prints ms per iteration, peak memory, and the MSE and LNCC similarity (1 - loss) before and after.
 """
@@ -74,12 +74,13 @@ def objective(disp, fixed, moving, grid, k=7, lam=0.5):
     return fused_lncc_loss(warp(moving, disp, grid), fixed, k) + lam * diffusion(disp)
 
 
-def register(fixed, moving, grid, iters=150, lr=0.02, lam=0.5, k=7):
+def register(fixed, moving, grid, iters=150, lr=0.02, lam=0.5, k=7, capturable=False):
     """Adam on the displacement field; returns the field and ms per iteration (timed from the
     second iteration on: the first one carries one-time initialization of the backward kernels
-    and the optimizer state)."""
+    and the optimizer state). capturable selects Adam's graph-safe implementation (the one
+    register_graph must use; its arithmetic differs from the default one in the last bits)."""
     disp = torch.zeros(1, 3, *fixed.shape[2:], device=fixed.device, requires_grad=True)
-    opt = torch.optim.Adam([disp], lr=lr)
+    opt = torch.optim.Adam([disp], lr=lr, capturable=capturable)
     t0 = None
     for i in range(iters):
         if i == 1:
@@ -91,6 +92,38 @@ def register(fixed, moving, grid, iters=150, lr=0.02, lam=0.5, k=7):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) / (iters - 1) * 1e3 if t0 is not None else float("nan")
     return disp.detach(), ms
+
+
+def register_graph(fixed, moving, grid, iters=150, lr=0.02, lam=0.5, k=7):
+    """The same optimization with one iteration (objective, backward, Adam step) captured in a HIP
+    graph and replayed: the host's per-iteration work (autograd, dozens of small launches) is gone,
+    which is most of an iteration at 96^3. Returns the field and ms per iteration (replays only)."""
+    disp = torch.zeros(1, 3, *fixed.shape[2:], device=fixed.device, requires_grad=True)
+    opt = torch.optim.Adam([disp], lr=lr, capturable=True)
+    # warm up on a side stream (allocates Adam's state), then start from zero again
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            opt.zero_grad(set_to_none=False)
+            objective(disp, fixed, moving, grid, k, lam).backward()
+            opt.step()
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.no_grad():
+        disp.zero_()
+        for st in opt.state[disp].values():
+            st.zero_()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        opt.zero_grad(set_to_none=False)  # a fill kernel, replayed with the rest
+        objective(disp, fixed, moving, grid, k, lam).backward()
+        opt.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        g.replay()
+    torch.cuda.synchronize()
+    return disp.detach().clone(), (time.perf_counter() - t0) / iters * 1e3
 
 
 @torch.no_grad()
@@ -105,15 +138,17 @@ def main():
     ap.add_argument("--size", type=int, default=96)
     ap.add_argument("--iters", type=int, default=150)
     ap.add_argument("--k", type=int, default=7)
+    ap.add_argument("--graph", action="store_true", help="replay one captured iteration (HIP graph)")
     a = ap.parse_args()
     fixed, moving, grid = make_pair(a.size, "cuda")
     zero = torch.zeros(1, 3, a.size, a.size, a.size, device="cuda")
     mse0, sim0 = quality(fixed, moving, zero, grid, a.k)
     torch.cuda.reset_peak_memory_stats()
-    disp, ms = register(fixed, moving, grid, a.iters, k=a.k)
+    disp, ms = (register_graph if a.graph else register)(fixed, moving, grid, a.iters, k=a.k)
     peak = torch.cuda.max_memory_allocated() / 1e9
     mse1, sim1 = quality(fixed, moving, disp, grid, a.k)
-    print(f"{a.size}^3, {a.iters} Adam iterations, k={a.k}: {ms:.2f} ms/iter, peak {peak:.2f} GB")
+    mode = "graph replay" if a.graph else "eager"
+    print(f"{a.size}^3, {a.iters} Adam iterations ({mode}), k={a.k}: {ms:.2f} ms/iter, peak {peak:.2f} GB")
     print(f"  before: MSE {mse0:.4e}  LNCC similarity {sim0:.4f}")
     print(f"  after:  MSE {mse1:.4e}  LNCC similarity {sim1:.4f}")
 
