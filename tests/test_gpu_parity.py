@@ -381,3 +381,27 @@ def test_workload_large_properties():
         assert rel < 1e-6
         del ps, gs
     assert abs(np.mean(parts) - L) <= 1e-6 * L
+
+
+def test_bf16_rounding_is_round_to_nearest_even():
+    """The bf16 gradient store rounds like torch's float32 -> bfloat16 (round to nearest, ties to
+    even; NaN stays NaN; the reference's store_g, fused_lncc/csrc/lncc3d.cu:21), checked bit for bit
+    through the bf16 grad *= grad_out kernel on a million random products, exact half-way cases,
+    infinities and NaN."""
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(1 << 20, generator=g) * torch.exp(8 * torch.randn(1 << 20, generator=g))).to(torch.bfloat16)
+    special = torch.tensor([1.0, -1.0, 2.0, 0.5, float("inf"), float("-inf"), float("nan"), 0.0, -0.0],
+                           dtype=torch.bfloat16)
+    x[: special.numel()] = special
+    for s in (0.7310586, 1.0 + 2.0 ** -8, -3.25):  # 1 + 2^-8 puts powers of two exactly half-way
+        out = x.to(DEV).clone()
+        ext.scale_grad_(out, torch.tensor(s, device=DEV))
+        torch.cuda.synchronize()
+        want = (x.float() * torch.tensor(s, dtype=torch.float32)).to(torch.bfloat16)
+        got = out.cpu()
+        nan = torch.isnan(want)
+        assert torch.equal(torch.isnan(got), nan)
+        # products in the float32 denormal range are left out (the device's float32 mode decides them)
+        tiny = want.float().abs() < 2.0 ** -126
+        keep = ~nan & ~tiny
+        assert torch.equal(got[keep].view(torch.int16), want[keep].view(torch.int16))
