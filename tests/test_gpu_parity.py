@@ -405,3 +405,22 @@ def test_bf16_rounding_is_round_to_nearest_even():
         tiny = want.float().abs() < 2.0 ** -126
         keep = ~nan & ~tiny
         assert torch.equal(got[keep].view(torch.int16), want[keep].view(torch.int16))
+
+
+def test_under_bf16_autocast():
+    """As the reference's README notes: under bf16 autocast the loss takes the bf16 activations
+    directly and the gradient reaches the model's parameters; float16 is refused (cast first)."""
+    torch.manual_seed(0)
+    net = torch.nn.Conv3d(1, 1, 3, padding=1).to(DEV)
+    x = torch.randn(1, 1, 16, 18, 20, device=DEV)
+    t = torch.randn(1, 1, 16, 18, 20, device=DEV)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = net(x)
+        assert y.dtype == torch.bfloat16
+        loss = fused_lncc_loss(y, t.bfloat16(), 5)
+    loss.backward()
+    assert loss.dtype == torch.float32 and torch.isfinite(loss)
+    assert net.weight.grad is not None and torch.isfinite(net.weight.grad).all()
+    assert net.weight.grad.abs().sum() > 0
+    with pytest.raises(RuntimeError, match="float32 or bfloat16"):
+        fused_lncc_loss(y.detach().half(), t.half(), 5)
