@@ -33,7 +33,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="headline", choices=["headline", "bf16", "mri", "large"])
+    ap.add_argument("--workload", default="headline", choices=["headline", "bf16", "mri", "large", "cpu"])
     ap.add_argument("--kernel-reps", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
