@@ -1,31 +1,37 @@
 """The reference's naive PyTorch LNCC restated (dense box-sum + autograd) — TEST/BASELINE ONLY.
 
-Follows baselines/torch_lncc.py:12-37 (``_box_dense``: one grouped ``F.conv3d`` with a ones
-kernel and zero padding k//2; ``_lncc``: cross, var_p, var_t with dr, ncc clamped at 1,
-loss 1 - mean). It is the CPU baseline leg of bench.py and is pinned to the reference by the
-golden vectors in tests/test_oracle.py. The product path never imports it.
+Follows baselines/torch_lncc.py:12-37: zero-padded k^3 box sums from a dense grouped convolution
+with a kernel of ones (padding k//2), cross = Spt - Sp St/n, variances with dr added and no clamp,
+ncc clamped at 1, loss 1 - mean. One convolution per field, as in the reference (a single
+convolution over the five stacked fields takes a grouped path that is several times slower on the
+CPU, which would misstate the baseline). It is the CPU baseline leg of bench.py and is pinned to
+the reference by the golden vectors in tests/test_oracle.py. The product path never imports it.
 """
 import torch
 import torch.nn.functional as F
 
 
 def box_dense(x, k):
-    c = x.shape[1]
-    return F.conv3d(x, x.new_ones(c, 1, k, k, k), padding=k // 2, groups=c)
+    """Zero-padded k^3 box sum of every channel of an (N, C, D, H, W) tensor."""
+    ones = torch.ones((x.shape[1], 1, k, k, k), dtype=x.dtype, device=x.device)
+    return F.conv3d(x, ones, padding=k // 2, groups=x.shape[1])
 
 
 def lncc_dense(pred, target, kernel_size=7, smooth_dr=1e-5):
+    """1 - mean(squared local NCC) with autograd to both inputs."""
     n = kernel_size ** 3
-    sp, st = box_dense(pred, kernel_size), box_dense(target, kernel_size)
-    cross = box_dense(pred * target, kernel_size) - sp * st / n
-    vp = box_dense(pred * pred, kernel_size) - sp * sp / n + smooth_dr
-    vt = box_dense(target * target, kernel_size) - st * st / n + smooth_dr
-    ncc = ((cross * cross) / (vp * vt)).clamp(max=1.0)
+    fields = (pred, target, pred * target, pred * pred, target * target)
+    s_p, s_t, s_pt, s_pp, s_tt = (box_dense(f, kernel_size) for f in fields)
+    cov = s_pt - s_p * s_t / n
+    var_p = s_pp - s_p * s_p / n + smooth_dr
+    var_t = s_tt - s_t * s_t / n + smooth_dr
+    ncc = torch.clamp(cov * cov / (var_p * var_t), max=1.0)
     return 1.0 - ncc.mean()
 
 
 def loss_and_grad(pred, target, kernel_size=7, smooth_dr=1e-5):
+    """The loss and its gradient with respect to pred (target held fixed)."""
     p = pred.detach().clone().requires_grad_(True)
     loss = lncc_dense(p, target, kernel_size, smooth_dr)
-    loss.backward()
-    return loss.detach(), p.grad
+    (grad,) = torch.autograd.grad(loss, p)
+    return loss.detach(), grad
