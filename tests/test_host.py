@@ -71,6 +71,15 @@ def test_errors_before_device_work():
     # the adjoint maps are all given or all omitted
     rc = lib.fl_lncc_maps(8, 8, 0, 1, 8, 8, 8, 7, 1e-5, 8, 8, None, 8, None)
     assert rc == _lib.FL_E_NULL and "all NULL" in lib.fl_last_error().decode()
+    # both gradients: every pointer is required, the workspace is checked on the one-pass path
+    # (k <= 7) and on the two-pass path (k = 9), and the shape before either
+    for k in (3, 7, 9):
+        rc = lib.fl_lncc_loss_grad_pt(8, 8, 0, 1, 8, 8, 8, k, 1e-5, 8, 8, None, 8, 64, None)
+        assert rc == _lib.FL_E_NULL and "NULL" in lib.fl_last_error().decode()
+        rc = lib.fl_lncc_loss_grad_pt(8, 8, 0, 1, 8, 8, 8, k, 1e-5, 8, 8, 8, 8, 0, None)
+        assert rc == _lib.FL_E_WORKSPACE and "workspace needs" in lib.fl_last_error().decode()
+    assert lib.fl_lncc_loss_grad_pt(8, 8, 0, 1, 0, 8, 8, 7, 1e-5, 8, 8, 8, 8, 64, None) == _lib.FL_E_SHAPE
+    assert lib.fl_lncc_loss_grad_pt(8, 8, 2, 1, 8, 8, 8, 7, 1e-5, 8, 8, 8, 8, 64, None) == _lib.FL_E_DTYPE
 
 
 def test_workspace_bytes():
