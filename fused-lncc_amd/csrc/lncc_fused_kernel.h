@@ -277,17 +277,200 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const int zq_lo = zlo + K - 1, zq_hi = min(D + K - 1, zhi - 1);  // old plane zi+1-K: zi in [zq_lo, zq_hi)
     constexpr int ZO = 2 + 2 * HH;                 // AZ: output plane zi-ZO
 
+    // Stage bodies; the march below orders them per phase.
+    //
+    // Y(zi-1): box sums S (y-sums of the rows of the five x-sums), then ncc and the adjoint
+    // coefficients at plane zcY (y_math).
+    auto y_math = [&](const float (&S)[5][G::SY], int zcY) __attribute__((always_inline)) {
+        const bool count = zcY >= z0 && zcY < z1;
+        float lsum = -0.f;  // -0 + x == x for every x, so the first add folds away
+#pragma unroll
+        for (int i = 0; i < G::SY; ++i) {
+            const int ay = y_start + i;
+            const float Sp = S[0][i], St = S[1][i], Spp = S[2][i], Stt = S[3][i], Spt = S[4][i];
+            const float mp = Sp * inv_n, mt = St * inv_n;
+            const float cross = fmaf(-mp, St, Spt);
+            const float vp = fmaxf(fmaf(-mp, Sp, Spp), 0.f) + dr;
+            const float vt = fmaxf(fmaf(-mt, St, Stt), 0.f) + dr;
+            const float rr = __builtin_amdgcn_rcpf(vp * vt);
+            const float cr = cross * rr;
+            const float ncc = cross * cr;
+            const bool live = y_inv[i] && (ncc < 1.0f);
+            const float nccc = (ncc >= 1.0f) ? 1.0f : ncc;
+            if (count && y_core[i]) lsum += nccc;
+            if constexpr (ADJ) {
+                // masking cr masks all three coefficients (alpha, beta, gamma are multiples of it)
+                const float crm = live ? cr : 0.f;
+                const float uu = crm * vt;
+                const float w = fmaf(-Sp, uu, St);
+                Gs[0 * G::GP + ay * G::GS + y_ax] = crm * w;
+                Gs[1 * G::GP + ay * G::GS + y_ax] = crm * uu;
+                Gs[2 * G::GP + ay * G::GS + y_ax] = crm;
+                if constexpr (DUAL) {  // the same with p and t swapped
+                    const float ut = crm * vp;
+                    const float wt = fmaf(-St, ut, Sp);
+                    Gs[3 * G::GP + ay * G::GS + y_ax] = crm * wt;
+                    Gs[4 * G::GP + ay * G::GS + y_ax] = crm * ut;
+                }
+            }
+            if constexpr (MODE == MODE_MAPS) {
+                if (count && y_core[i]) {
+                    const float uu = cr * vt;
+                    const float w = fmaf(-Sp, uu, St);
+                    const int gx = x0 - HH + y_ax, gy = y0 - HH + ay;
+                    const int64_t o = ((b * D + zcY) * Hd + gy) * (int64_t)Wd + gx;
+                    a.ncc_map[o] = nccc;
+                    if (a.a_map) {  // null: the ncc map alone
+                        a.a_map[o] = live ? -2.f * inv_n * (cr * w) : 0.f;
+                        a.b_map[o] = live ? -(cr * uu) : 0.f;
+                        a.c_map[o] = live ? 2.f * cr : 0.f;
+                    }
+                }
+            }
+        }
+        loss_acc += (double)lsum;
+    };
+    // F(zi): z-sums of the input region. Consume the planes prefetched one step ago, then prefetch
+    // the next ones. Every global access of the loop is issued unconditionally (inactive ones
+    // through a zero-sized buffer), so the number of outstanding memory operations is the same on
+    // every path and the waits before use stay exact. With STORE the z-sums go to the LDS column
+    // by column as they are formed; without, f_store writes them later.
+    auto f_sums = [&](auto rc, auto store, int zi, uint64_t zoff) __attribute__((always_inline)) {
+        constexpr int r = decltype(rc)::value;
+        constexpr bool STORE = decltype(store)::value;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            // plane zi replaces plane zi-k (ring slot r; the ring starts at zero: nothing before
+            // the first plane of the march was added)
+            const float p = pnext[j], t = tnext[j];
+            float po, to;
+            if constexpr (RING) {
+                po = pring[r][j];
+                to = tring[r][j];
+                pring[r][j] = p;
+                tring[r][j] = t;
+            } else {
+                po = pold[j];
+                to = told[j];
+            }
+            zsum[j][0] += p - po;
+            zsum[j][1] += t - to;
+            zsum[j][2] = fmaf(p, p, fmaf(-po, po, zsum[j][2]));
+            zsum[j][3] = fmaf(t, t, fmaf(-to, to, zsum[j][3]));
+            zsum[j][4] = fmaf(p, t, fmaf(-po, to, zsum[j][4]));
+            if constexpr (STORE) {
+                if (zaddr[j] >= 0) {
+#pragma unroll
+                    for (int q = 0; q < 5; ++q) Zs[q * G::ZP + zaddr[j]] = zsum[j][q];
+                }
+            }
+        }
+        // prefetch plane zi+1 (and, without the ring, plane zi+1-k leaving the window)
+        const bool okn = zi + 1 < zn_hi;
+        const __amdgpu_buffer_rsrc_t rpn = rsrc_at(pva + zoff + PB, plane_bytes, okn);
+        const __amdgpu_buffer_rsrc_t rtn = rsrc_at(tva + zoff + PB, plane_bytes, okn);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            pnext[j] = load_elem<BF16>(rpn, voff[j]);
+            tnext[j] = load_elem<BF16>(rtn, voff[j]);
+        }
+        if constexpr (!RING) {
+            // non-temporal: the last use of the halo columns' lines in this tile (the central ones
+            // are re-read once more by AZ two steps later); marked evict-first they leave the L2
+            // to the planes that are still to be re-read
+            const bool okq = zi >= zq_lo && zi < zq_hi;
+            const __amdgpu_buffer_rsrc_t rpq = rsrc_at(pva + zoff - (K - 1) * PB, plane_bytes, okq);
+            const __amdgpu_buffer_rsrc_t rtq = rsrc_at(tva + zoff - (K - 1) * PB, plane_bytes, okq);
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                pold[j] = load_elem<BF16, kNT>(rpq, voff[j]);
+                told[j] = load_elem<BF16, kNT>(rtq, voff[j]);
+            }
+        }
+    };
+    auto f_store = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            if (zaddr[j] >= 0) {
+#pragma unroll
+                for (int q = 0; q < 5; ++q) Zs[q * G::ZP + zaddr[j]] = zsum[j][q];
+            }
+        }
+    };
+    // X(zi) or AX(zi-1), the lane's unit: x-sums of one z-sum (feeds Y at the next plane) or of
+    // one of alpha, beta, gamma at plane zcY, over one segment. Either in one piece (u_whole), or
+    // with the row read early and the sums formed by u_math later; the early read takes SX + 2h
+    // floats for both kinds (SX >= SA), and an AX row's extra floats stay inside Gs, unused.
+    static_assert(G::U1 == 1 && G::SX >= G::SA, "one unit per lane");
+    auto u_whole = [&](bool runX, bool runA) __attribute__((always_inline)) {
+        if (runX) {
+            float v[G::SX + 2 * HH], o[G::SX];
+            lds_row(Zs + u_src[0], v);
+            window_sums<HH, G::SX>(v, o);
+#pragma unroll
+            for (int i = 0; i < G::SX; ++i) Xs[u_dst[0] + i * G::XS] = o[i];
+        } else if (runA) {
+            float v[G::SA + 2 * HH], o[G::SA];
+            lds_row(Gs + u_src[0], v);
+            window_sums<HH, G::SA>(v, o);
+#pragma unroll
+            for (int i = 0; i < G::SA; ++i) GXs[u_dst[0] + i * G::XS] = o[i];
+        }
+    };
+    auto u_math = [&](const float (&uv)[G::SX + 2 * HH], bool runX, bool runA) __attribute__((always_inline)) {
+        if (runX) {
+            float o[G::SX];
+            window_sums<HH, G::SX>(uv, o);
+#pragma unroll
+            for (int i = 0; i < G::SX; ++i) Xs[u_dst[0] + i * G::XS] = o[i];
+        } else if (runA) {
+            float v[G::SA + 2 * HH], o[G::SA];
+#pragma unroll
+            for (int i = 0; i < G::SA + 2 * HH; ++i) v[i] = uv[i];
+            window_sums<HH, G::SA>(v, o);
+#pragma unroll
+            for (int i = 0; i < G::SA; ++i) GXs[u_dst[0] + i * G::XS] = o[i];
+        }
+    };
+
+    // Stage order inside a phase. Each wave runs its stages in program order, so a stage placed
+    // between the issue of another stage's LDS reads and their use hides part of their latency.
+    // Measured at (2,16,128^3):
+    //  * P0, k <= 5, one gradient: Y's rows, then F's arithmetic and prefetch, then Y's math, AYs
+    //    and F's stores (k = 5: -7%). At k >= 7, and with both gradients, the rows held across F
+    //    exceed the 128-register budget of a 1024-lane workgroup (spills), and F stays last.
+    //  * P1: AZ's xy-sums are read before everything else (-2%), and the unit's row is read
+    //    before AZ and its sums formed after AZ. With both gradients at k <= 5 the plain order
+    //    (the unit, then AZ with its reads) measured 4% faster and is kept there.
+    constexpr bool F_EARLY = HH <= 2 && !DUAL;
+    constexpr bool P1_PLAIN = HH <= 2 && DUAL;
+
     for (int base = zlo; base < zhi; base += K) {
         static_for<0, K>([&](auto rc) __attribute__((always_inline)) {
-            constexpr int r = decltype(rc)::value;
-            const int zi = base + r;
+            const int zi = base + decltype(rc)::value;
             if (zi >= zhi) return;
+            const int zcY = zi - 1 - HH;   // Y(zi-1) and AX(zi-1)
+            const bool actY = zcY >= zc_lo && zcY < zc_hi;
+            const int zcB = zi - 2 - HH;   // AYs(zi-2) and the xy-sums AZ(zi-2) reads
+            const bool actB = ADJ && zcB >= zc_lo && zcB < zc_hi;
 
             // ============================ phase P0 ============================
-            // Y(zi-1): box sums, ncc, adjoint coefficients at plane zcY
-            const int zcY = zi - 1 - HH;
-            const bool actY = zcY >= zc_lo && zcY < zc_hi;
-            if (actY && has_y) {
+            // Y(zi-1), AYs(zi-2), F(zi)
+            if constexpr (F_EARLY) {
+                float yv[5][G::SY + 2 * HH];
+                if (actY && has_y) {
+#pragma unroll
+                    for (int q = 0; q < 5; ++q) lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv[q]);
+                }
+                f_sums(rc, std::false_type{}, zi, zoff);
+                if (actY && has_y) {
+                    float S[5][G::SY];
+#pragma unroll
+                    for (int q = 0; q < 5; ++q) window_sums<HH, G::SY>(yv[q], S[q]);
+                    y_math(S, zcY);
+                }
+            } else if (actY && has_y) {
+                // one row at a time: all five held at once exceed the register budget here
                 float S[5][G::SY];
 #pragma unroll
                 for (int q = 0; q < 5; ++q) {
@@ -295,58 +478,10 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv);
                     window_sums<HH, G::SY>(yv, S[q]);
                 }
-                const bool count = zcY >= z0 && zcY < z1;
-                float lsum = -0.f;  // -0 + x == x for every x, so the first add folds away
-#pragma unroll
-                for (int i = 0; i < G::SY; ++i) {
-                    const int ay = y_start + i;
-                    const float Sp = S[0][i], St = S[1][i], Spp = S[2][i], Stt = S[3][i], Spt = S[4][i];
-                    const float mp = Sp * inv_n, mt = St * inv_n;
-                    const float cross = fmaf(-mp, St, Spt);
-                    const float vp = fmaxf(fmaf(-mp, Sp, Spp), 0.f) + dr;
-                    const float vt = fmaxf(fmaf(-mt, St, Stt), 0.f) + dr;
-                    const float rr = __builtin_amdgcn_rcpf(vp * vt);
-                    const float cr = cross * rr;
-                    const float ncc = cross * cr;
-                    const bool live = y_inv[i] && (ncc < 1.0f);
-                    const float nccc = (ncc >= 1.0f) ? 1.0f : ncc;
-                    if (count && y_core[i]) lsum += nccc;
-                    if constexpr (ADJ) {
-                        // masking cr masks all three coefficients (alpha, beta, gamma are multiples of it)
-                        const float crm = live ? cr : 0.f;
-                        const float uu = crm * vt;
-                        const float w = fmaf(-Sp, uu, St);
-                        Gs[0 * G::GP + ay * G::GS + y_ax] = crm * w;
-                        Gs[1 * G::GP + ay * G::GS + y_ax] = crm * uu;
-                        Gs[2 * G::GP + ay * G::GS + y_ax] = crm;
-                        if constexpr (DUAL) {  // the same with p and t swapped
-                            const float ut = crm * vp;
-                            const float wt = fmaf(-St, ut, Sp);
-                            Gs[3 * G::GP + ay * G::GS + y_ax] = crm * wt;
-                            Gs[4 * G::GP + ay * G::GS + y_ax] = crm * ut;
-                        }
-                    }
-                    if constexpr (MODE == MODE_MAPS) {
-                        if (count && y_core[i]) {
-                            const float uu = cr * vt;
-                            const float w = fmaf(-Sp, uu, St);
-                            const int gx = x0 - HH + y_ax, gy = y0 - HH + ay;
-                            const int64_t o = ((b * D + zcY) * Hd + gy) * (int64_t)Wd + gx;
-                            a.ncc_map[o] = nccc;
-                            if (a.a_map) {  // null: the ncc map alone
-                                a.a_map[o] = live ? -2.f * inv_n * (cr * w) : 0.f;
-                                a.b_map[o] = live ? -(cr * uu) : 0.f;
-                                a.c_map[o] = live ? 2.f * cr : 0.f;
-                            }
-                        }
-                    }
-                }
-                loss_acc += (double)lsum;
+                y_math(S, zcY);
             }
-            // AYs(zi-2): y-sums of alpha, beta, gamma at plane zcB (one quantity per unit)
-            const int zcB = zi - 2 - HH;
-            const bool actB = ADJ && zcB >= zc_lo && zcB < zc_hi;
             if constexpr (ADJ) {
+                // AYs(zi-2): y-sums of alpha, beta, gamma at plane zcB (one quantity per unit)
                 if (actB && has_b) {
                     float v[G::SB + 2 * HH], o[G::SB];
                     lds_row(GXs + b_src, v);
@@ -355,116 +490,62 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     for (int i = 0; i < G::SB; ++i) GY[b_dst + i * G::GYS] = o[i];
                 }
             }
-            // F(zi): z-sums of the input region. Consume the planes prefetched one step ago, then
-            // prefetch the next ones. Every global access of the loop is issued unconditionally
-            // (inactive ones through a zero-sized buffer), so the number of outstanding memory
-            // operations is the same on every path and the waits before use stay exact.
-            {
-#pragma unroll
-                for (int j = 0; j < J; ++j) {
-                    // plane zi replaces plane zi-k (ring slot r; the ring starts at zero: nothing
-                    // before the first plane of the march was added)
-                    const float p = pnext[j], t = tnext[j];
-                    float po, to;
-                    if constexpr (RING) {
-                        po = pring[r][j];
-                        to = tring[r][j];
-                        pring[r][j] = p;
-                        tring[r][j] = t;
-                    } else {
-                        po = pold[j];
-                        to = told[j];
-                    }
-                    zsum[j][0] += p - po;
-                    zsum[j][1] += t - to;
-                    zsum[j][2] = fmaf(p, p, fmaf(-po, po, zsum[j][2]));
-                    zsum[j][3] = fmaf(t, t, fmaf(-to, to, zsum[j][3]));
-                    zsum[j][4] = fmaf(p, t, fmaf(-po, to, zsum[j][4]));
-                    if (zaddr[j] >= 0) {
-#pragma unroll
-                        for (int q = 0; q < 5; ++q) Zs[q * G::ZP + zaddr[j]] = zsum[j][q];
-                    }
-                }
-                // prefetch plane zi+1 (and, without the ring, plane zi+1-k leaving the window)
-                const bool okn = zi + 1 < zn_hi;
-                const __amdgpu_buffer_rsrc_t rpn = rsrc_at(pva + zoff + PB, plane_bytes, okn);
-                const __amdgpu_buffer_rsrc_t rtn = rsrc_at(tva + zoff + PB, plane_bytes, okn);
-#pragma unroll
-                for (int j = 0; j < J; ++j) {
-                    pnext[j] = load_elem<BF16>(rpn, voff[j]);
-                    tnext[j] = load_elem<BF16>(rtn, voff[j]);
-                }
-                if constexpr (!RING) {
-                    // non-temporal: the last use of the halo columns' lines in this tile (the
-                    // central ones are re-read once more by AZ two steps later); marked evict-first
-                    // they leave the L2 to the planes that are still to be re-read
-                    const bool okq = zi >= zq_lo && zi < zq_hi;
-                    const __amdgpu_buffer_rsrc_t rpq = rsrc_at(pva + zoff - (K - 1) * PB, plane_bytes, okq);
-                    const __amdgpu_buffer_rsrc_t rtq = rsrc_at(tva + zoff - (K - 1) * PB, plane_bytes, okq);
-#pragma unroll
-                    for (int j = 0; j < J; ++j) {
-                        pold[j] = load_elem<BF16, kNT>(rpq, voff[j]);
-                        told[j] = load_elem<BF16, kNT>(rtq, voff[j]);
-                    }
-                }
+            if constexpr (F_EARLY) {
+                f_store();
+            } else {
+                f_sums(rc, std::true_type{}, zi, zoff);
             }
             __syncthreads();
 
             // ============================ phase P1 ============================
-            // X(zi) and AX(zi-1): x-sums of the z-sums (feeds Y at the next plane) and of alpha,
-            // beta, gamma at plane zcY, one quantity of one segment per unit
+            // X(zi) and AX(zi-1) on the unit lanes, AZ(zi-2) on the output lanes
+            float ys[NA];
+            auto read_ys = [&]() __attribute__((always_inline)) {
+#pragma unroll
+                for (int c = 0; c < NA; ++c) ys[c] = actB ? GY[c * G::GYP + z_oy * G::GYS + z_ox] : 0.f;
+            };
+            if constexpr (ADJ && !P1_PLAIN) read_ys();
             const int zcX = zi - HH;
             const bool actX = zcX >= zc_lo && zcX < zc_hi;
-#pragma unroll
-            for (int k = 0; k < G::U1; ++k) {
-                if (u_kind[k] == 1 && actX) {
-                    float v[G::SX + 2 * HH], o[G::SX];
-                    lds_row(Zs + u_src[k], v);
-                    window_sums<HH, G::SX>(v, o);
-#pragma unroll
-                    for (int i = 0; i < G::SX; ++i) Xs[u_dst[k] + i * G::XS] = o[i];
-                } else if (ADJ && u_kind[k] == 2 && actY) {
-                    float v[G::SA + 2 * HH], o[G::SA];
-                    lds_row(Gs + u_src[k], v);
-                    window_sums<HH, G::SA>(v, o);
-#pragma unroll
-                    for (int i = 0; i < G::SA; ++i) GXs[u_dst[k] + i * G::XS] = o[i];
-                }
+            const bool runX = u_kind[0] == 1 && actX, runA = ADJ && u_kind[0] == 2 && actY;
+            float uv[G::SX + 2 * HH];
+            if constexpr (P1_PLAIN) {
+                u_whole(runX, runA);
+            } else if (runX || runA) {
+                lds_row((runA ? Gs : Zs) + u_src[0], uv);
             }
             if constexpr (ADJ) {
                 // AZ(zi-2): z ring of the xy-sums, combine at the output plane zo (lanes without an
                 // output column run on a clamped one and store out of range, i.e. nothing)
-                {
-                    float ys[NA];
+                constexpr int r = decltype(rc)::value;
+                if constexpr (P1_PLAIN) read_ys();
 #pragma unroll
-                    for (int c = 0; c < NA; ++c) ys[c] = actB ? GY[c * G::GYP + z_oy * G::GYS + z_ox] : 0.f;
-#pragma unroll
-                    for (int c = 0; c < NA; ++c) {
-                        gz[c] += ys[c] - gring[c][r];
-                        gring[c][r] = ys[c];
-                    }
-                    const int zo = zi - ZO;
-                    const float g = a.gscale * fmaf(inv_n, gz[0], fmaf(pz, gz[1], -tzz * gz[2]));
-                    // Non-temporal: the gradient is never read back, and this re-read of p,t is the
-                    // last use of those lines. With the default policy both would be promoted in the
-                    // L2 and push out the planes that F loaded and this stage re-reads 2h+2 steps
-                    // later, so that every input byte would be fetched about twice; marked
-                    // evict-first, every input byte is fetched from HBM once. bf16 gradient rows
-                    // of a tile are half a 128-byte line (the x-neighbour tile writes the other
-                    // half): those stores keep the default policy, so that the L2 merges the two
-                    // halves into one write.
-                    store_elem_buf<BF16, BF16 ? 0 : kNT>(rsrc_at(gva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, g);
-                    if constexpr (DUAL) {
-                        const float gt = a.gscale * fmaf(inv_n, gz[3], fmaf(tzz, gz[4], -pz * gz[2]));
-                        store_elem_buf<BF16, BF16 ? 0 : kNT>(rsrc_at(tgva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, gt);
-                    }
-                    // prefetch p,t at the next step's output plane; issued after this step's use, so
-                    // one register each suffices and no copy has to wait for the load
-                    const bool oko = zo + 1 >= z0 && zo + 1 < z1;
-                    pz = load_elem<BF16, kNT>(rsrc_at(pva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
-                    tzz = load_elem<BF16, kNT>(rsrc_at(tva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
+                for (int c = 0; c < NA; ++c) {
+                    gz[c] += ys[c] - gring[c][r];
+                    gring[c][r] = ys[c];
                 }
+                const int zo = zi - ZO;
+                const float g = a.gscale * fmaf(inv_n, gz[0], fmaf(pz, gz[1], -tzz * gz[2]));
+                // Non-temporal: the gradient is never read back, and this re-read of p,t is the
+                // last use of those lines. With the default policy both would be promoted in the
+                // L2 and push out the planes that F loaded and this stage re-reads 2h+2 steps
+                // later, so that every input byte would be fetched about twice; marked
+                // evict-first, every input byte is fetched from HBM once. bf16 gradient rows of a
+                // tile are half a 128-byte line (the x-neighbour tile writes the other half):
+                // those stores keep the default policy, so that the L2 merges the two halves into
+                // one write.
+                store_elem_buf<BF16, BF16 ? 0 : kNT>(rsrc_at(gva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, g);
+                if constexpr (DUAL) {
+                    const float gt = a.gscale * fmaf(inv_n, gz[3], fmaf(tzz, gz[4], -pz * gz[2]));
+                    store_elem_buf<BF16, BF16 ? 0 : kNT>(rsrc_at(tgva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, gt);
+                }
+                // prefetch p,t at the next step's output plane; issued after this step's use, so
+                // one register each suffices and no copy has to wait for the load
+                const bool oko = zo + 1 >= z0 && zo + 1 < z1;
+                pz = load_elem<BF16, kNT>(rsrc_at(pva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
+                tzz = load_elem<BF16, kNT>(rsrc_at(tva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
             }
+            if constexpr (!P1_PLAIN) u_math(uv, runX, runA);
             zoff += PB;
             __syncthreads();
         });
