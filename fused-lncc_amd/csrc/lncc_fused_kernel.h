@@ -437,8 +437,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // between the issue of another stage's LDS reads and their use hides part of their latency.
     // Measured at (2,16,128^3):
     //  * P0, k <= 5, one gradient: Y's rows, then F's arithmetic and prefetch, then Y's math, AYs
-    //    and F's stores (k = 5: -7%). At k >= 7, and with both gradients, the rows held across F
-    //    exceed the 128-register budget of a 1024-lane workgroup (spills), and F stays last.
+    //    and F's stores (k = 5: -7%). At k >= 7 the rows held across F exceed the 128-register
+    //    budget of a 1024-lane workgroup (spills), and with both gradients the reorder measured
+    //    slower (k = 3: +12%): there F stays last.
     //  * P1: AZ's xy-sums are read before everything else (-2%), and the unit's row is read
     //    before AZ and its sums formed after AZ. With both gradients at k <= 5 the plain order
     //    (the unit, then AZ with its reads) measured 4% faster and is kept there.
