@@ -54,28 +54,6 @@ __device__ __forceinline__ void lds_row(const float* __restrict__ src, float (&v
     }
 }
 
-// Lane order for work over n_rows rows of LEN (>= 32) positions: indices [0, 32 n_rows) take
-// positions 0..31 of one row per 32 consecutive lanes, so that each half-wave stores into a
-// single destination row (consecutive LDS banks, no conflicts); the remaining indices take
-// positions 32..LEN-1 row after row.
-template <int LEN>
-__device__ __forceinline__ void split32(int idx, int n_rows, int& row, int& pos) {
-    static_assert(LEN >= 32, "rows of at least 32 positions");
-    if constexpr (LEN == 32) {
-        row = idx >> 5;
-        pos = idx & 31;
-    } else {
-        if (idx < 32 * n_rows) {
-            row = idx >> 5;
-            pos = idx & 31;
-        } else {
-            const int e = idx - 32 * n_rows;
-            row = e / (LEN - 32);
-            pos = 32 + e % (LEN - 32);
-        }
-    }
-}
-
 // Running window sums of width 2H+1: out[i] = v[i] + ... + v[i+2H] for i < S.
 template <int H, int S>
 __device__ __forceinline__ void window_sums(const float (&v)[S + 2 * H], float (&out)[S]) {
@@ -139,45 +117,23 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     int zaddr[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const int c = tid + j * NT;
+        int ix, iy;
         voff[j] = kOOB;
         zaddr[j] = -1;
-        if (c < G::NIN) {
-            const int iy = c / G::IX, ix = c - iy * G::IX;
+        if (f_column<G>(tid + j * NT, ix, iy, zaddr[j])) {
             const int gx = x0 - 2 * HH + ix, gy = y0 - 2 * HH + iy;
             if (gx >= 0 && gx < Wd && gy >= 0 && gy < Hd) voff[j] = (uint32_t)((gy * Wd + gx) * ELEM);
-            zaddr[j] = iy * G::ZS + ix;
         }
     }
     // P1 units: X (z-sums -> x-sums) then AX (adjoints -> x-sums); offsets into the source and
     // destination buffers and the unit kind (0 none, 1 X, 2 AX)
     int u_src[G::U1], u_dst[G::U1], u_kind[G::U1];
 #pragma unroll
-    for (int k = 0; k < G::U1; ++k) {
-        const int u = tid + k * NT;
-        u_kind[k] = 0;
-        u_src[k] = 0;
-        u_dst[k] = 0;
-        if (u < G::UX) {
-            int row, iy;  // rows (q, seg) of IY positions
-            split32<G::IY>(u, 5 * G::XSEG, row, iy);
-            const int q = row / G::XSEG, start = (row % G::XSEG) * G::SX;
-            u_kind[k] = 1;
-            u_src[k] = q * G::ZP + iy * G::ZS + start;
-            u_dst[k] = q * G::XP + start * G::XS + iy;
-        } else if (ADJ && u >= G::AX_LANE0 && u < G::AX_LANE0 + G::UA) {
-            int row, ay;  // rows (c, seg) of AY positions
-            split32<G::AY>(u - G::AX_LANE0, NA * G::ASEG, row, ay);
-            const int c = row / G::ASEG, start = (row % G::ASEG) * G::SA;
-            u_kind[k] = 2;
-            u_src[k] = c * G::GP + ay * G::GS + start;
-            u_dst[k] = c * G::GXP + start * G::GXS + ay;
-        }
-    }
+    for (int k = 0; k < G::U1; ++k) u_kind[k] = p1_unit<G, ADJ>(tid + k * NT, u_src[k], u_dst[k]);
     // P0: Y items on lanes [0, YITEMS), AYs units on waves 10, 11, 14, 15 (and 6 with five fields)
     const bool has_y = tid < G::YITEMS;
     int y_seg = 0, y_ax = 0;  // rows seg of AX positions
-    if (has_y) split32<G::AX>(tid, G::YSEG, y_seg, y_ax);
+    if (has_y) y_item<G>(tid, y_seg, y_ax);
     const int y_start = y_seg * G::SY;
     // per output of the Y segment: inside the volume (ncc and adjoints live) / counted in the loss
     // (inside the volume and in the output tile); the same on every plane
@@ -193,29 +149,11 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             y_core[i] = y_inv[i] && corex && ay >= HH && ay < HH + TY;
         }
     }
-    const int wave = tid >> 6;
-    const int bslot = wave == 10 ? 0 : wave == 11 ? 1 : wave == 14 ? 2 : wave == 15 ? 3 : (DUAL && wave == 6) ? 4 : -1;
-    const bool has_b = ADJ && bslot >= 0 && (tid & 63) < G::B_PER_WAVE;
-    int b_src = 0, b_dst = 0;
-    if (has_b) {
-        // rows (c, seg) of TX = 32 positions. Three fields: slot s takes row s on its first 32
-        // lanes and half of row 4 + s/2 on the next 16. Five fields: slot s takes both rows of
-        // field s (32 lanes each).
-        const int l = tid & 63;
-        int row, ox;
-        if constexpr (DUAL) {
-            row = 2 * bslot + (l >> 5);
-            ox = l & 31;
-        } else {
-            row = l < 32 ? bslot : 4 + (bslot >> 1);
-            ox = l < 32 ? l : (bslot & 1) * 16 + (l - 32);
-        }
-        const int c = row / G::BSEG, start = (row % G::BSEG) * G::SB;
-        b_src = c * G::GXP + ox * G::GXS + start;
-        b_dst = c * G::GYP + start * G::GYS + ox;
-    }
+    int b_src, b_dst;
+    const bool has_b = ays_unit<G>(tid, b_src, b_dst) && ADJ;
     const bool has_z = ADJ && tid < G::NOUT;
-    const int z_ox = tid % TX, z_oy = min(tid / TX, TY - 1);
+    int z_ox, z_oy;
+    az_lane(tid, z_ox, z_oy);
     const bool z_in = has_z && x0 + z_ox < Wd && y0 + z_oy < Hd;
     const uint32_t z_voff = z_in ? (uint32_t)(((y0 + z_oy) * Wd + x0 + z_ox) * ELEM) : kOOB;
 
@@ -414,7 +352,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             lds_row(Gs + u_src[0], v);
             window_sums<HH, G::SA>(v, o);
 #pragma unroll
-            for (int i = 0; i < G::SA; ++i) GXs[u_dst[0] + i * G::XS] = o[i];
+            for (int i = 0; i < G::SA; ++i) GXs[u_dst[0] + i * G::GXS] = o[i];
         }
     };
     auto u_math = [&](const float (&uv)[G::SX + 2 * HH], bool runX, bool runA) __attribute__((always_inline)) {
@@ -429,7 +367,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             for (int i = 0; i < G::SA + 2 * HH; ++i) v[i] = uv[i];
             window_sums<HH, G::SA>(v, o);
 #pragma unroll
-            for (int i = 0; i < G::SA; ++i) GXs[u_dst[0] + i * G::XS] = o[i];
+            for (int i = 0; i < G::SA; ++i) GXs[u_dst[0] + i * G::GXS] = o[i];
         }
     };
 

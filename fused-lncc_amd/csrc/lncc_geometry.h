@@ -1,0 +1,188 @@
+// Tile geometry and per-lane work maps of the fused LNCC kernel. Plain C++ (no HIP builtins):
+// the kernel takes every LDS offset it uses from these functions, and the host-side model of the
+// kernel's LDS accesses (tests/lds_model.cpp) enumerates the same functions for every lane.
+#pragma once
+
+#if defined(__HIPCC__)
+#define FL_HD __host__ __device__
+#else
+#define FL_HD
+#endif
+
+namespace fl {
+
+// Workgroup: 1024 lanes (16 wave64s, one workgroup per CU). Output tile: TX x TY columns of one
+// volume, marched along D.
+constexpr int NT = 1024;
+constexpr int WG_PER_CU = 1;
+constexpr int TX = 32;
+constexpr int TY = 32;
+
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
+constexpr int odd(int a) { return a | 1; }
+
+// Row stride (floats) for LDS rows read as float4 by lanes that step from row to row: = 4 mod 8,
+// so that the 8 lanes served per cycle by a 128-bit read land on distinct groups of 4 banks.
+constexpr int stride4(int n) { return n + ((12 - n % 8) % 8); }
+constexpr int rup4(int n) { return (n + 3) / 4 * 4; }
+constexpr int rup64(int n) { return (n + 63) / 64 * 64; }
+
+// Tile geometry for halo H (k = 2H+1). Coordinates inside a workgroup:
+//   input region   ix in [0,IX), iy in [0,IY)  <-> global (x0-2H+ix, y0-2H+iy)
+//   adjoint region ax in [0,AX), ay in [0,AY)  <-> global (x0-H+ax,  y0-H+ay)
+//   output tile    ox in [0,TX), oy in [0,TY)  <-> global (x0+ox,    y0+oy)
+// Running-sum passes work on segments of S consecutive outputs. The X and Y passes round their
+// output range up to whole segments: the extra outputs read row padding and land in padding rows
+// of the destination that no later pass reads (and that the loss never counts), so no lane needs
+// a per-output store mask.
+// NA = number of adjoint fields carried from Y to AZ: 3 (alpha, beta, gamma of the pred gradient)
+// or 5 (with alpha', beta' of the target gradient; gamma is shared)
+template <int H, int NA = 3>
+struct Geo {
+    static constexpr int HALO = H, NADJ = NA;
+    static constexpr int K = 2 * H + 1;
+    static constexpr int TY = fl::TY;
+    static constexpr int IX = TX + 4 * H, IY = TY + 4 * H;
+    static constexpr int AX = TX + 2 * H, AY = TY + 2 * H;
+    static constexpr int NIN = IX * IY;
+    static constexpr int J = cdiv(NIN, NT);               // input columns per lane
+    static constexpr int NOUT = TX * TY;                  // output columns (one lane each)
+    // X: x-sums of the five z-sums; items (iy, seg) over rows iy < IY, outputs ax < XR (>= AX)
+    static constexpr int SX = rup4(cdiv(AX, 2)), XSEG = 2, XR = XSEG * SX, XITEMS = IY * XSEG;
+    // Y: y-sums -> box sums, ncc, adjoints; items (ax, seg), outputs ay < YR (>= AY)
+    static constexpr int SY = 4, YSEG = cdiv(AY, SY), YR = YSEG * SY, YITEMS = AX * YSEG;
+    // AX: x-sums of alpha, beta, gamma; items (ay, seg), outputs ox < TX
+    static constexpr int SA = 16, ASEG = TX / SA, AITEMS = AY * ASEG;
+    // AYs: y-sums of the three; items (ox, seg), outputs oy < TY
+    static constexpr int SB = TY / 2, BSEG = TY / SB, BITEMS = TX * BSEG;
+    // Work units of the running-sum passes are single quantities of one segment. Waves are
+    // spread over the 4 SIMDs of the CU round-robin (wave w on SIMD w % 4), so the heavy items
+    // are placed to even out each SIMD's share of a phase: in phase P1 the X units (5 per item)
+    // fill the first waves and the AX units (3 per item) start on the next wave boundary; in
+    // phase P0 the Y items fill the first waves (SIMDs 0 and 1 get the extra ones) and the AYs
+    // units (3 per item) go to waves 10, 11, 14, 15 (SIMDs 2 and 3), B_PER_WAVE each.
+    // With five adjoint fields the AYs units (two rows of 32 per field) take five whole waves.
+    static constexpr int UX = 5 * XITEMS, UA = NA * AITEMS, AX_LANE0 = rup64(UX), U1 = 1;
+    static constexpr int UB = NA * BITEMS, B_PER_WAVE = NA == 3 ? UB / 4 : 64;
+    static_assert(YITEMS <= 10 * 64 && AX_LANE0 + UA <= NT && BSEG == 2 && TX == 32 &&
+                      (NA == 3 ? (UB == 192 && B_PER_WAVE == 48) : (NA == 5 && UB == 320)),
+                  "lanes");
+    // every segment starts on a 16-byte boundary (rows are read as float4)
+    static_assert(XR >= AX && TX % SA == 0 && TY % SB == 0 && SX % 4 == 0 && SY % 4 == 0 &&
+                      SA % 4 == 0 && SB % 4 == 0, "segments");
+    // LDS layout (floats): Zs[5][IY][ZS], XsT[5][XR][XS] (transposed), Gs[NA][YR][GS],
+    // GXsT[NA][TX][GXS] (transposed), GY[NA][TY][GYS]; each buffer but GY ends in PAD spare floats
+    static constexpr int ZS = stride4(IX), XS = stride4(cmax(IY, AY)), GS = stride4(AX), GXS = XS;
+    static constexpr int GYS = TX + 1, PAD = 16;
+    static constexpr int ZP = IY * ZS, XP = XR * XS, GP = YR * GS, GXP = TX * GXS, GYP = TY * GYS;
+    // A segment reads rup4(S + 2H) floats from its start; reads past a row's end stay inside the
+    // buffer (the next row or the spare floats) and only feed outputs that are never used.
+    static_assert(SX + rup4(SX + 2 * H) <= ZS + PAD && YR - SY + rup4(SY + 2 * H) <= XS + PAD &&
+                      TX - SA + rup4(SA + 2 * H) <= GS + PAD && TY - SB + rup4(SB + 2 * H) <= GXS + PAD,
+                  "row reads");
+    static constexpr int LDS_FLOATS = 5 * (ZP + XP) + NA * (GP + GXP + GYP) + 4 * PAD;
+    static_assert(LDS_FLOATS * 4 <= 160 * 1024, "LDS");
+};
+
+// Lane order for work over n_rows rows of LEN (>= 32) positions: indices [0, 32 n_rows) take
+// positions 0..31 of one row per 32 consecutive lanes, so that each half-wave stores into a
+// single destination row (consecutive LDS banks, no conflicts); the remaining indices take
+// positions 32..LEN-1 row after row.
+template <int LEN>
+FL_HD inline void split32(int idx, int n_rows, int& row, int& pos) {
+    static_assert(LEN >= 32, "rows of at least 32 positions");
+    if constexpr (LEN == 32) {
+        row = idx >> 5;
+        pos = idx & 31;
+    } else {
+        if (idx < 32 * n_rows) {
+            row = idx >> 5;
+            pos = idx & 31;
+        } else {
+            const int e = idx - 32 * n_rows;
+            row = e / (LEN - 32);
+            pos = 32 + e % (LEN - 32);
+        }
+    }
+}
+
+// F: input column c (lane + j * NT) of the input region, if c < NIN: its position (ix, iy) and
+// the offset of its z-sum in each of the five Zs planes.
+template <class G>
+FL_HD inline bool f_column(int c, int& ix, int& iy, int& zaddr) {
+    if (c >= G::NIN) return false;
+    iy = c / G::IX;
+    ix = c - iy * G::IX;
+    zaddr = iy * G::ZS + ix;
+    return true;
+}
+
+// P1 unit of lane u: 1 = X (x-sums of one z-sum over one segment of row iy: reads Zs from src,
+// writes Xs at dst + i * XS), 2 = AX (x-sums of one adjoint field over one segment of row ay:
+// reads Gs from src, writes GXs at dst + i * GXS), 0 = none.
+template <class G, bool ADJ>
+FL_HD inline int p1_unit(int u, int& src, int& dst) {
+    src = 0;
+    dst = 0;
+    if (u < G::UX) {
+        int row, iy;  // rows (q, seg) of IY positions
+        split32<G::IY>(u, 5 * G::XSEG, row, iy);
+        const int q = row / G::XSEG, start = (row % G::XSEG) * G::SX;
+        src = q * G::ZP + iy * G::ZS + start;
+        dst = q * G::XP + start * G::XS + iy;
+        return 1;
+    }
+    if (ADJ && u >= G::AX_LANE0 && u < G::AX_LANE0 + G::UA) {
+        int row, ay;  // rows (c, seg) of AY positions
+        split32<G::AY>(u - G::AX_LANE0, G::NADJ * G::ASEG, row, ay);
+        const int c = row / G::ASEG, start = (row % G::ASEG) * G::SA;
+        src = c * G::GP + ay * G::GS + start;
+        dst = c * G::GXP + start * G::GXS + ay;
+        return 2;
+    }
+    return 0;
+}
+
+// Y item of lane tid < YITEMS: adjoint column ax and segment seg (rows y_start = seg * SY ...).
+// It reads Xs at q * XP + ax * XS + y_start and writes Gs at c * GP + (y_start + i) * GS + ax.
+template <class G>
+FL_HD inline void y_item(int tid, int& seg, int& ax) {
+    split32<G::AX>(tid, G::YSEG, seg, ax);
+}
+
+// AYs unit of lane tid, on waves 10, 11, 14, 15 (and 6 with five fields), B_PER_WAVE lanes each:
+// y-sums of one adjoint field over one segment of output column ox; reads GXs from src, writes GY
+// at dst + i * GYS. Returns false for lanes without a unit.
+template <class G>
+FL_HD inline bool ays_unit(int tid, int& src, int& dst) {
+    constexpr bool five = G::NADJ == 5;
+    src = 0;
+    dst = 0;
+    const int wave = tid >> 6, l = tid & 63;
+    const int bslot = wave == 10 ? 0 : wave == 11 ? 1 : wave == 14 ? 2 : wave == 15 ? 3 : (five && wave == 6) ? 4 : -1;
+    if (bslot < 0 || l >= G::B_PER_WAVE) return false;
+    // rows (c, seg) of TX = 32 positions. Three fields: slot s takes row s on its first 32 lanes
+    // and half of row 4 + s/2 on the next 16. Five fields: slot s takes both rows of field s.
+    int row, ox;
+    if constexpr (five) {
+        row = 2 * bslot + (l >> 5);
+        ox = l & 31;
+    } else {
+        row = l < 32 ? bslot : 4 + (bslot >> 1);
+        ox = l < 32 ? l : (bslot & 1) * 16 + (l - 32);
+    }
+    const int c = row / G::BSEG, start = (row % G::BSEG) * G::SB;
+    src = c * G::GXP + ox * G::GXS + start;
+    dst = c * G::GYP + start * G::GYS + ox;
+    return true;
+}
+
+// AZ: output column (ox, oy) of lane tid (lanes beyond the tile run on a clamped row); it reads
+// GY at c * GYP + oy * GYS + ox.
+FL_HD inline void az_lane(int tid, int& ox, int& oy) {
+    ox = tid % TX;
+    oy = tid / TX < TY - 1 ? tid / TX : TY - 1;
+}
+
+}  // namespace fl
