@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <atomic>
 #include <string>
 
 #include "../../include/fused_lncc.h"
@@ -30,6 +31,21 @@ struct Plan {
     uint32_t nblocks;
 };
 
+// Compute units of the current device, read once per device (256 on an MI355X in its
+// single-partition mode, fewer in a partitioned one); 256 when no device is visible, so that
+// host-only callers (the workspace-size query in a build environment) still get a plan.
+int device_cus() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cache[kMaxDevices];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
 // Workgroups: B volumes x (W/TX) x (H/TY) tiles x D-chunks. A chunk of d output planes costs
 // d + 4h + 2 pipeline steps (it recomputes the halo planes of its neighbours), so D is split only
 // where that shortens the launch: small volumes, whose tiles alone leave CUs idle, get short chunks;
@@ -41,9 +57,9 @@ Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     p.nty = (int)((H + ty - 1) / ty);
     const int64_t base = B * p.ntx * p.nty;
     // Split D into nzc chunks. A chunk of d planes costs d + 4h + 2 pipeline steps, and the
-    // workgroups run in rounds of one per CU (MI355X: 256 CUs): pick the split with the fewest
-    // rounds x steps (ties: fewer workgroups).
-    const int64_t kCUs = 256;
+    // workgroups run in rounds of one per CU: pick the split with the fewest rounds x steps (ties:
+    // fewer workgroups).
+    const int64_t kCUs = device_cus();
     int64_t best_cost = -1, dchunk = D;
     for (int64_t nzc = 1; nzc <= D; ++nzc) {
         const int64_t d = (D + nzc - 1) / nzc;

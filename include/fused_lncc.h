@@ -54,7 +54,8 @@ int fl_validate(int dtype, int kernel_size, int64_t B, int64_t D, int64_t H, int
  */
 size_t fl_lds_bytes(int kernel_size, int dtype);
 
-/* Device bytes of the workspace fl_lncc_loss_grad needs for this shape (per-workgroup partials). */
+/* Device bytes of the workspace fl_lncc_loss_grad needs for this shape (per-workgroup partials),
+ * for the current device: the launch plan follows the device's compute-unit count. */
 size_t fl_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size);
 
 /*

@@ -205,6 +205,14 @@ def test_nonfinite_input_gives_nonfinite_loss(bad):
     assert not torch.isfinite(loss).item()
 
 
+def test_plan_follows_device_cus():
+    """The D-chunk plan is made for the device's compute units: the MRI-shaped volume (42 tiles of
+    32 x 32 per plane) is split into as many chunks as fill the CUs in one round."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    nblocks = ext.workspace_bytes((1, 160, 192, 224), 9) // 8
+    assert nblocks % 42 == 0 and nblocks <= cus < nblocks + 42, (nblocks, cus)
+
+
 def test_many_volumes():
     """N*C = 2080 volumes of (128, 8, 8) (tests/test_fixes.py:9-17)."""
     p, t = wl.randn_pair((2080, 1, 128, 8, 8), 8)
