@@ -308,6 +308,41 @@ def test_no_grad_and_target_grad():
     assert td.grad is None and pd.grad is not None
 
 
+def test_concurrent_host_threads():
+    """Re-entrancy of the C ABI: four host threads, each on its own stream with its own inputs,
+    workspace and outputs, call the library at the same time (ctypes releases the GIL during the
+    call); every result is bitwise the one the same call gives alone."""
+    import threading
+    cases = [(wl.randn_pair((1, 2, 20 + 3 * i, 30, 26 + i), 40 + i), 3 + 2 * (i % 4)) for i in range(4)]
+    inputs = [(p.to(DEV).reshape(-1, *p.shape[2:]), t.to(DEV).reshape(-1, *t.shape[2:]), k) for (p, t), k in cases]
+    alone = []
+    for pf, tf, k in inputs:
+        loss, grad = ext.loss_grad(pf, tf, k, 1e-5)
+        alone.append((loss.item(), grad.cpu()))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in inputs]
+    got = [None] * len(inputs)
+    start = threading.Barrier(len(inputs))
+
+    def work(i):
+        pf, tf, k = inputs[i]
+        with torch.cuda.stream(streams[i]):
+            start.wait()
+            for _ in range(20):
+                loss, grad = ext.loss_grad(pf, tf, k, 1e-5)
+            streams[i].synchronize()
+            got[i] = (loss.item(), grad.cpu())
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(len(inputs))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert all(not th.is_alive() for th in threads)
+    for (l0, g0), (l1, g1) in zip(alone, got):
+        assert l0 == l1 and torch.equal(g0, g1)
+
+
 def test_side_stream_and_determinism():
     p, t = wl.randn_pair((2, 3, 40, 36, 44), 11)
     l1, g1, _ = fused(p, t, 7)
