@@ -1,7 +1,8 @@
 """ctypes front-end of the CPU oracle (``liblncc_oracle.so``) — TEST INFRASTRUCTURE ONLY.
 
 Only the tests, ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` import this
-module, as the checker. The product path (the ``fused_lncc`` package) never imports it.
+module, as the reference the results are compared with. The product path (the ``fused_lncc``
+package) never imports it.
 """
 import ctypes
 import os

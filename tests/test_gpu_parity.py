@@ -1,7 +1,7 @@
 """GPU parity of the HIP path against the reference's golden vectors and the CPU oracle.
 
 Mirrors the reference's own tests (tests/test_pytest.py, test_fixes.py, test_robust.py,
-test_bf16.py, verify_fwd.py, verify_bwd.py) with the north-star bar:
+test_bf16.py, verify_fwd.py, verify_bwd.py) with the parity bar:
   fp32 loss relative error <= 1e-5, bf16 loss relative error <= 1e-2,
   gradient cosine > 0.9999 and relative L2 error < 1e-3.
 Inputs are generated on the CPU (seeded), so every run sees the same bytes.
@@ -306,6 +306,54 @@ def test_no_grad_and_target_grad():
     pd = p.to(DEV).requires_grad_(True)
     fused_lncc_loss(pd, td, 7).backward()
     assert td.grad is None and pd.grad is not None
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_maximum_plane_size(dtype):
+    """Planes just under the 2 GiB limit of the per-plane (31-bit) offsets: 16384 x 32767 float32 or
+    32768 x 32767 bfloat16, two planes, all zero but a random patch in the far corner (the highest
+    offsets). Zero data and zero padding are the same to the box sums, so the corner holds exactly
+    the problem of a small volume with the patch and a 2h+2 zero margin: its gradient equals the
+    small volume's scaled by the voxel-count ratio (the oracle pins the small one), and every other
+    gradient voxel of the plane is exactly zero."""
+    k, h = 7, 3
+    H, W, D = (16384, 32767, 2) if dtype == torch.float32 else (32768, 32767, 2)
+    assert H * W * (4 if dtype == torch.float32 else 2) < 2 ** 31
+    ph, pw, m = 24, 40, 2 * h + 2
+    p, t = wl.randn_pair((1, 1, D, ph, pw), 77)
+    p, t = p.to(dtype), t.to(dtype)
+    ps = torch.zeros(1, D, ph + m, pw + m, dtype=dtype)
+    ts = torch.zeros_like(ps)
+    ps[0, :, m:, m:], ts[0, :, m:, m:] = p[0, 0], t[0, 0]
+    loss_s, g_s = ext.loss_grad(ps.to(DEV), ts.to(DEV), k, 1e-5)
+    lr, gr = O.lncc(ps.float().numpy(), ts.float().numpy(), k)
+    assert abs(loss_s.item() - lr) <= (1e-5 if dtype == torch.float32 else 1e-2) * abs(lr)
+    assert_grad(gr, g_s.double().cpu().numpy(), 0.9999 if dtype == torch.float32 else 0.999,
+                1e-3 if dtype == torch.float32 else 2e-2)
+
+    print(f"max plane: {dtype} ({D}, {H}, {W})", flush=True)
+    pb = torch.zeros(1, D, H, W, dtype=dtype, device=DEV)
+    tb = torch.zeros_like(pb)
+    pb[0, :, H - ph:, W - pw:] = p[0, 0].to(DEV)
+    tb[0, :, H - ph:, W - pw:] = t[0, 0].to(DEV)
+    loss_b, g_b = ext.loss_grad(pb, tb, k, 1e-5)
+    del pb, tb
+    corner = g_b[0, :, H - ph - m:, W - pw - m:].double().cpu().numpy()
+    scale = (D * H * W) / float(D * (ph + m) * (pw + m))
+    ref = g_s[0].double().cpu().numpy() / scale
+    cos = float((corner * ref).sum() / (np.linalg.norm(corner) * np.linalg.norm(ref)))
+    rel = float(np.linalg.norm(corner - ref) / np.linalg.norm(ref))
+    if dtype == torch.float32:
+        assert cos > 0.99999 and rel < 1e-4, (cos, rel)
+    else:  # both gradients are rounded to bf16 once, at different scales
+        assert cos > 0.9999 and rel < 1e-2, (cos, rel)
+    g_b[0, :, H - ph - m:, W - pw - m:] = 0
+    assert g_b.abs().max().item() == 0.0
+    # the ncc sum of the plane is the small volume's; the float32 loss 1 - sum/M is within one
+    # rounding step (2^-24 below 1) of its value, which at this M is worth 2^-24 M in the sum
+    s_b = (1.0 - loss_b.item()) * D * H * W
+    s_s = (1.0 - loss_s.item()) * D * (ph + m) * (pw + m)
+    assert abs(s_b - s_s) <= 2.0 ** -24 * D * H * W + 1e-3 * abs(s_s), (s_b, s_s)
 
 
 def test_concurrent_host_threads():

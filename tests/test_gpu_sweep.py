@@ -1,5 +1,5 @@
 """Randomized parity sweep: many small shapes (edges smaller than the halo, one-plane volumes,
-ragged tiles), every kernel size, both dtypes, against the CPU oracle with the north-star bar.
+ragged tiles), every kernel size, both dtypes, against the CPU oracle with the parity bar.
 The second sweep asks for both gradients (target_grad=True: the one-pass kernel for k <= 7, two
 passes for k = 9) and forces short D-chunks on some cases, so chunk seams land inside the volume.
 Seeded, so every run draws the same cases; each case prints its parameters on failure."""

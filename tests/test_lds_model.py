@@ -5,7 +5,7 @@ counts, from the lane maps the kernel itself uses (fused-lncc_amd/csrc/lncc_geom
 
 This is the stand-in for the reference's compute-sanitizer workloads (tests/_sanitize*.py): GPU
 address sanitizers are not available for LDS and ROCm has no LDS race checker. Each planted
-mistake (a model-side perturbation of one lane map) must be reported, so the checker is known to
+mistake (a model-side perturbation of one lane map) must be reported, so the model is known to
 see the kinds of error it is for."""
 import os
 import shutil

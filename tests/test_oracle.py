@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/lncc_oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/lncc_oracle.c) before the GPU results are compared with it.
 
 * golden vectors written from the reference's own torch LNCC (baselines/torch_lncc.py:12-42):
   loss and autograd gradient on full small tensors, loss plus gradient checksums at the
