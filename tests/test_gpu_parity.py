@@ -308,6 +308,30 @@ def test_no_grad_and_target_grad():
     assert td.grad is None and pd.grad is not None
 
 
+@pytest.mark.parametrize("k", [3, 5, 7, 9])
+def test_regression_2x8x40(k):
+    """The reference's regression at (2,8,40^3) fp32 (tests/test_fixes.py:26-35,
+    tests/test_bf16.py:22-29: |dl| < 1e-4, cosine > 0.9999, loss in [0, 1]), with the parity bar."""
+    p, t = wl.randn_pair((2, 8, 40, 40, 40), 12 + k)
+    loss, g, _ = fused(p, t, k)
+    lr, gr = O.lncc(p.numpy(), t.numpy(), k)
+    assert abs(loss - lr) < 1e-4 and 0.0 <= loss <= 1.0
+    assert_loss(loss, lr, LOSS_RTOL_F32)
+    assert_grad(g, gr)
+
+
+def test_large_shape_finite():
+    """The reference's large-shape run (tests/test_robust.py:52-59): (2,32,128^3) forward + backward
+    gives a finite loss in [0, 1] and a finite gradient."""
+    gen = torch.Generator(device=DEV).manual_seed(13)
+    t = torch.randn(2, 32, 128, 128, 128, device=DEV, generator=gen)
+    p = (0.8 * t + 0.6 * torch.randn(t.shape, device=DEV, generator=gen)).requires_grad_(True)
+    loss = fused_lncc_loss(p, t, 7)
+    loss.backward()
+    assert 0.0 <= loss.item() <= 1.0
+    assert torch.isfinite(p.grad).all().item()
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_maximum_plane_size(dtype):
     """Planes just under the 2 GiB limit of the per-plane (31-bit) offsets: 16384 x 32767 float32 or
