@@ -12,6 +12,7 @@ namespace fl {
 
 constexpr int BT = 16;      // box kernel output tile BT x BT, one lane per output column
 constexpr int BNT = BT * BT;
+static_assert(BNT == kBoxLanes, "box launch shape");
 
 template <int HH, int NF, bool BF16>
 __global__ __launch_bounds__(BNT) void box_kernel(BoxArgs a) {

@@ -13,6 +13,7 @@
 namespace {
 
 thread_local std::string g_err;
+thread_local int64_t t_dchunk_override = 0;  // fl_test_set_dchunk; 0 = the planner's choice
 
 int fail(int code, const std::string& msg) {
     g_err = msg;
@@ -28,7 +29,7 @@ constexpr int64_t kMaxPlaneBytes = 0x7fffffffLL;  // per-plane buffer offsets ar
 
 struct Plan {
     int ntx, nty, nzc, dchunk;
-    uint32_t nblocks;
+    int64_t nblocks;
 };
 
 // Compute units of the current device, read once per device (256 on an MI355X in its
@@ -48,11 +49,12 @@ int device_cus() {
 
 // Workgroups: B volumes x (W/TX) x (H/TY) tiles x D-chunks. A chunk of d output planes costs
 // d + 4h + 2 pipeline steps (it recomputes the halo planes of its neighbours), so D is split only
-// where that shortens the launch: small volumes, whose tiles alone leave CUs idle, get short chunks;
-// FUSED_LNCC_DCHUNK overrides the chunk length for tuning.
+// where that shortens the launch: small volumes, whose tiles alone leave CUs idle, get short chunks.
+// fl_test_set_dchunk fixes the chunk length for the calling thread (tests of chunk seams and of
+// long unsplit marches).
 Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     Plan p;
-    const int ty = fl::TY;
+    const int ty = fl::tile_rows(halo);
     p.ntx = (int)((W + fl::TX - 1) / fl::TX);
     p.nty = (int)((H + ty - 1) / ty);
     const int64_t base = B * p.ntx * p.nty;
@@ -71,15 +73,15 @@ Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
         }
         if (blocks >= 8 * kCUs) break;
     }
-    if (const char* e = getenv("FUSED_LNCC_DCHUNK")) {
-        const long v = strtol(e, nullptr, 10);
-        if (v > 0) dchunk = v < D ? v : D;
-    }
+    if (t_dchunk_override > 0) dchunk = t_dchunk_override < D ? t_dchunk_override : D;
     p.dchunk = (int)dchunk;
     p.nzc = (int)((D + dchunk - 1) / dchunk);
-    p.nblocks = (uint32_t)(base * p.nzc);
+    p.nblocks = base * p.nzc;
     return p;
 }
+
+// A launch of n workgroups of `lanes` lanes: the grid in lanes must fit in 32 bits.
+bool grid_fits(int64_t n, int lanes) { return n >= 1 && n <= (int64_t)0xffffffffLL / lanes; }
 
 // elem = bytes per element of the volumes; callers that do not know the dtype (workspace size,
 // finalize) pass the smallest, 2, and the launch that reads the volumes checks its own dtype.
@@ -87,15 +89,16 @@ int check_shape(int64_t B, int64_t D, int64_t H, int64_t W, int elem) {
     if (B < 1 || D < 1 || H < 1 || W < 1) return fail(FL_E_SHAPE, "fused_lncc: empty volume (B, D, H, W must be >= 1)");
     if (H > kMaxPlaneBytes || W > kMaxPlaneBytes || H * W * elem > kMaxPlaneBytes)
         return fail(FL_E_SHAPE, "fused_lncc: one (H, W) plane exceeds 2 GiB");
-    if (D > (1 << 30)) return fail(FL_E_SHAPE, "fused_lncc: D too large");
-    // workgroups of the largest launch plan (32 x 32 tiles, one per plane): a 31-bit grid,
-    // multiplied up factor by factor so that no product can overflow
-    int64_t tiles = B;
-    const int64_t factors[3] = {(W + fl::TX - 1) / fl::TX, (H + fl::TY - 1) / fl::TY, D};
-    for (int64_t f : factors) {
-        if (tiles > 0x7fffffffLL / f) return fail(FL_E_SHAPE, "fused_lncc: too many volumes/tiles for one launch");
-        tiles *= f;
-    }
+    if (D > (1 << 30) || B > (1LL << 40))
+        return fail(FL_E_SHAPE, "fused_lncc: too many planes or volumes (D <= 2^30, B <= 2^40)");
+    return FL_OK;
+}
+
+// The fused kernel's smallest plan (one workgroup per tile and volume, D unsplit) must fit one
+// launch; the products stay far inside int64 after check_shape's limits.
+int check_grid(int64_t B, int64_t H, int64_t W, int halo) {
+    const int64_t tiles = B * ((W + fl::TX - 1) / fl::TX) * ((H + fl::tile_rows(halo) - 1) / fl::tile_rows(halo));
+    if (!grid_fits(tiles, fl::NT)) return fail(FL_E_SHAPE, "fused_lncc: too many volumes/tiles for one launch");
     return FL_OK;
 }
 
@@ -121,11 +124,48 @@ hipError_t launch_fused(int halo, int mode, bool bf16, const fl::FusedArgs& a, u
     }
 }
 
+// Kernel arguments shared by every mode of the fused kernel; mode-specific outputs are set by the
+// caller.
+fl::FusedArgs fused_args(const void* pred, const void* target, int64_t B, int64_t D, int64_t H, int64_t W,
+                         int kernel_size, float smooth_dr, const Plan& p) {
+    const double M = (double)B * (double)D * (double)H * (double)W;
+    const double n = (double)kernel_size * kernel_size * kernel_size;
+    fl::FusedArgs a = {};
+    a.pred = pred;
+    a.target = target;
+    a.dimD = (int)D;
+    a.dimH = (int)H;
+    a.dimW = (int)W;
+    a.ntx = p.ntx;
+    a.nty = p.nty;
+    a.nzc = p.nzc;
+    a.dchunk = p.dchunk;
+    a.inv_n = (float)(1.0 / n);
+    a.nf = (float)n;
+    a.ndr = (float)n * smooth_dr;
+    a.gscale = (float)(2.0 * n / M);
+    return a;
+}
+
+// The fused kernel's plan for this call, checked against the 32-bit grid limit (a forced short
+// chunk can multiply the workgroups of a plan).
+int planned(int64_t B, int64_t D, int64_t H, int64_t W, int halo, Plan& p, const char* who) {
+    p = plan_fused(B, D, H, W, halo);
+    if (!grid_fits(p.nblocks, fl::NT)) return fail(FL_E_SHAPE, std::string(who) + ": too many workgroups for one launch");
+    return FL_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int fl_version(void) { return (0 << 16) | (1 << 8) | 0; }
+int fl_version(void) { return (0 << 16) | (2 << 8) | 0; }
+
+int fl_test_set_dchunk(int planes) {
+    if (planes < 0) return fail(FL_E_SHAPE, "fl_test_set_dchunk: negative chunk length");
+    t_dchunk_override = planes;
+    return FL_OK;
+}
 
 const char* fl_last_error(void) { return g_err.c_str(); }
 
@@ -134,7 +174,9 @@ int fl_validate(int dtype, int kernel_size, int64_t B, int64_t D, int64_t H, int
     if (rc) return rc;
     rc = check_k(kernel_size);
     if (rc) return rc;
-    return check_shape(B, D, H, W, dtype == FL_BF16 ? 2 : 4);
+    rc = check_shape(B, D, H, W, dtype == FL_BF16 ? 2 : 4);
+    if (rc) return rc;
+    return check_grid(B, H, W, kernel_size / 2);
 }
 
 size_t fl_lds_bytes(int kernel_size, int dtype) {
@@ -152,8 +194,10 @@ size_t fl_lds_bytes(int kernel_size, int dtype) {
 }
 
 size_t fl_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size) {
-    if (check_k(kernel_size) || check_shape(B, D, H, W, 2)) return 0;
-    return (size_t)plan_fused(B, D, H, W, kernel_size / 2).nblocks * sizeof(double);
+    if (check_k(kernel_size) || check_shape(B, D, H, W, 2) || check_grid(B, H, W, kernel_size / 2)) return 0;
+    Plan p;
+    if (planned(B, D, H, W, kernel_size / 2, p, "fl_workspace_bytes")) return 0;
+    return (size_t)p.nblocks * sizeof(double);
 }
 
 int fl_lncc_fused_partials(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,
@@ -163,27 +207,16 @@ int fl_lncc_fused_partials(const void* pred, const void* target, int dtype, int6
     if (rc) return rc;
     if (!pred || !target || !workspace) return fail(FL_E_NULL, "fl_lncc_fused_partials: NULL pointer argument");
     const int halo = kernel_size / 2;
-    const Plan p = plan_fused(B, D, H, W, halo);
+    Plan p;
+    rc = planned(B, D, H, W, halo, p, "fl_lncc_fused_partials");
+    if (rc) return rc;
     if (workspace_bytes < (size_t)p.nblocks * sizeof(double))
         return fail(FL_E_WORKSPACE, "fl_lncc_fused_partials: workspace needs " +
                                         std::to_string((size_t)p.nblocks * sizeof(double)) + " bytes");
-    const double M = (double)B * (double)D * (double)H * (double)W;
-    fl::FusedArgs a = {};
-    a.pred = pred;
-    a.target = target;
+    fl::FusedArgs a = fused_args(pred, target, B, D, H, W, kernel_size, smooth_dr, p);
     a.grad = grad;
     a.partials = static_cast<double*>(workspace);
-    a.dimD = (int)D;
-    a.dimH = (int)H;
-    a.dimW = (int)W;
-    a.ntx = p.ntx;
-    a.nty = p.nty;
-    a.nzc = p.nzc;
-    a.dchunk = p.dchunk;
-    a.inv_n = (float)(1.0 / ((double)kernel_size * kernel_size * kernel_size));
-    a.dr = smooth_dr;
-    a.gscale = (float)(2.0 / M);
-    hipError_t e = launch_fused(halo, grad ? fl::MODE_GRAD : fl::MODE_LOSS, dtype == FL_BF16, a, p.nblocks,
+    hipError_t e = launch_fused(halo, grad ? fl::MODE_GRAD : fl::MODE_LOSS, dtype == FL_BF16, a, (uint32_t)p.nblocks,
                                 static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "fl_lncc_fused_partials: fused kernel launch");
     return FL_OK;
@@ -193,9 +226,12 @@ int fl_lncc_finalize(const void* workspace, int64_t B, int64_t D, int64_t H, int
                      float* loss, void* stream) {
     int rc = check_k(kernel_size);
     if (!rc) rc = check_shape(B, D, H, W, 2);
+    if (!rc) rc = check_grid(B, H, W, kernel_size / 2);
     if (rc) return rc;
     if (!workspace || !loss) return fail(FL_E_NULL, "fl_lncc_finalize: NULL pointer argument");
-    const Plan p = plan_fused(B, D, H, W, kernel_size / 2);
+    Plan p;
+    rc = planned(B, D, H, W, kernel_size / 2, p, "fl_lncc_finalize");
+    if (rc) return rc;
     const double M = (double)B * (double)D * (double)H * (double)W;
     hipError_t e = fl::launch_finalize(static_cast<const double*>(workspace), (int)p.nblocks, 1.0 / M, loss,
                                        static_cast<hipStream_t>(stream));
@@ -223,40 +259,13 @@ int fl_lncc_loss_grad_pt(const void* pred, const void* target, int dtype, int64_
     if (rc) return rc;
     if (!pred || !target || !loss || !grad_pred || !grad_target || !workspace)
         return fail(FL_E_NULL, "fl_lncc_loss_grad_pt: NULL pointer argument");
-    const int halo = kernel_size / 2;
-    if (halo == 4) {
-        // five adjoint fields do not fit in LDS at k = 9: the pred pass, then the same kernel with
-        // pred and target swapped (the loss is symmetric); its partials are not reduced
-        rc = fl_lncc_loss_grad(pred, target, dtype, B, D, H, W, kernel_size, smooth_dr, loss, grad_pred, workspace,
-                               workspace_bytes, stream);
-        if (rc) return rc;
-        return fl_lncc_fused_partials(target, pred, dtype, B, D, H, W, kernel_size, smooth_dr, grad_target,
-                                      workspace, workspace_bytes, stream);
-    }
-    const Plan p = plan_fused(B, D, H, W, halo);
-    if (workspace_bytes < (size_t)p.nblocks * sizeof(double))
-        return fail(FL_E_WORKSPACE, "fl_lncc_loss_grad_pt: workspace needs " +
-                                        std::to_string((size_t)p.nblocks * sizeof(double)) + " bytes");
-    const double M = (double)B * (double)D * (double)H * (double)W;
-    fl::FusedArgs a = {};
-    a.pred = pred;
-    a.target = target;
-    a.grad = grad_pred;
-    a.tgrad = grad_target;
-    a.partials = static_cast<double*>(workspace);
-    a.dimD = (int)D;
-    a.dimH = (int)H;
-    a.dimW = (int)W;
-    a.ntx = p.ntx;
-    a.nty = p.nty;
-    a.nzc = p.nzc;
-    a.dchunk = p.dchunk;
-    a.inv_n = (float)(1.0 / ((double)kernel_size * kernel_size * kernel_size));
-    a.dr = smooth_dr;
-    a.gscale = (float)(2.0 / M);
-    hipError_t e = launch_fused(halo, fl::MODE_DUAL, dtype == FL_BF16, a, p.nblocks, static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return hip_fail(e, "fl_lncc_loss_grad_pt: fused kernel launch");
-    return fl_lncc_finalize(workspace, B, D, H, W, kernel_size, loss, stream);
+    // the pred pass with the loss, then the same kernel with pred and target swapped (the loss is
+    // symmetric in its inputs); the second pass's partials are not reduced
+    rc = fl_lncc_loss_grad(pred, target, dtype, B, D, H, W, kernel_size, smooth_dr, loss, grad_pred, workspace,
+                           workspace_bytes, stream);
+    if (rc) return rc;
+    return fl_lncc_fused_partials(target, pred, dtype, B, D, H, W, kernel_size, smooth_dr, grad_target, workspace,
+                                  workspace_bytes, stream);
 }
 
 int fl_scale_grad(void* grad, int dtype, int64_t n, const float* grad_out, void* stream) {
@@ -278,26 +287,16 @@ int fl_lncc_maps(const void* pred, const void* target, int dtype, int64_t B, int
     if (!pred || !target || !ncc || (adjoint_maps && !(A && Bc && Cc)))
         return fail(FL_E_NULL, "fl_lncc_maps: NULL pointer argument (A, Bc, Cc are all given or all NULL)");
     const int halo = kernel_size / 2;
-    const Plan p = plan_fused(B, D, H, W, halo);
-    fl::FusedArgs a = {};
-    a.pred = pred;
-    a.target = target;
+    Plan p;
+    rc = planned(B, D, H, W, halo, p, "fl_lncc_maps");
+    if (rc) return rc;
+    fl::FusedArgs a = fused_args(pred, target, B, D, H, W, kernel_size, smooth_dr, p);
     a.ncc_map = ncc;
     a.a_map = A;
     a.b_map = Bc;
     a.c_map = Cc;
-    a.partials = nullptr;
-    a.dimD = (int)D;
-    a.dimH = (int)H;
-    a.dimW = (int)W;
-    a.ntx = p.ntx;
-    a.nty = p.nty;
-    a.nzc = p.nzc;
-    a.dchunk = p.dchunk;
-    a.inv_n = (float)(1.0 / ((double)kernel_size * kernel_size * kernel_size));
-    a.dr = smooth_dr;
-    a.gscale = 0.f;
-    hipError_t e = launch_fused(halo, fl::MODE_MAPS, dtype == FL_BF16, a, p.nblocks, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_fused(halo, fl::MODE_MAPS, dtype == FL_BF16, a, (uint32_t)p.nblocks,
+                                static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "fl_lncc_maps: launch");
     return FL_OK;
 }
@@ -321,7 +320,7 @@ int fl_lncc_backward(const float* A, const float* Bc, const float* Cc, const voi
     a.ntx = (int)((W + 15) / 16);
     a.nty = (int)((H + 15) / 16);
     a.scale = scale;
-    if (B * a.ntx * a.nty > 0x7fffffffLL) return fail(FL_E_SHAPE, "fl_lncc_backward: too many volumes/tiles for one launch");
+    if (!grid_fits(B * a.ntx * a.nty, fl::kBoxLanes)) return fail(FL_E_SHAPE, "fl_lncc_backward: too many volumes/tiles for one launch");
     const uint32_t nb = (uint32_t)(B * a.ntx * a.nty);
     hipError_t e = fl::launch_box(kernel_size / 2, 3, dtype == FL_BF16, a, nb, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "fl_lncc_backward: launch");
@@ -341,7 +340,7 @@ int fl_box3d(const float* x, float* y, int64_t B, int64_t D, int64_t H, int64_t 
     a.ntx = (int)((W + 15) / 16);
     a.nty = (int)((H + 15) / 16);
     a.scale = 1.f;
-    if (B * a.ntx * a.nty > 0x7fffffffLL) return fail(FL_E_SHAPE, "fl_box3d: too many volumes/tiles for one launch");
+    if (!grid_fits(B * a.ntx * a.nty, fl::kBoxLanes)) return fail(FL_E_SHAPE, "fl_box3d: too many volumes/tiles for one launch");
     const uint32_t nb = (uint32_t)(B * a.ntx * a.nty);
     hipError_t e = fl::launch_box(kernel_size / 2, 1, false, a, nb, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "fl_box3d: launch");

@@ -4,39 +4,47 @@
 // marches along D over a chunk [z0,z1) of planes. Per input plane zi it runs six stages, lagged
 // along D so that every quantity is produced from data already on chip:
 //
-//   F   (registers) lanes own the input columns of the (TX+4h) x (TY+4h) region and keep running
-//       z-sums of p, t, p^2, t^2, p*t: add plane zi (prefetched one plane ahead), subtract plane
-//       zi-k (from a k-deep register ring of p,t; for k = 9 and in MODE_DUAL, where the ring does
-//       not fit the register budget, re-read from global memory, still cache resident, and
-//       prefetched too); write the five z-sums to LDS.
-//   X   running x-sums of the five z-sums over the (TX+2h)-wide adjoint range.
-//   Y   running y-sums -> the five k^3 box-sums on the (TX+2h) x (TY+2h) adjoint region; per voxel
+//   F   (registers) lanes own the input columns of the (TX+4h) x (TY+4h) region and keep the
+//       last k planes of p, t in a register ring; the z-sums of p, t, p^2, t^2, p*t over planes
+//       [zi-k+1, zi] are formed from the ring (below) and written to LDS.
+//   X   x-sums of the five z-sums over the (TX+2h)-wide adjoint range.
+//   Y   y-sums -> the five k^3 box-sums on the (TX+2h) x (TY+2h) adjoint region; per voxel
 //       squared NCC (clamped to 1), loss partial sums, and the adjoint coefficients alpha, beta,
 //       gamma (zero where ncc >= 1 or outside the volume).
-//   AX  running x-sums of alpha, beta, gamma over the TX output columns.
-//   AYs running y-sums of the three over the TY output rows.
-//   AZ  (registers) one lane per output column: k-deep ring of the xy-sums and running z-sums ->
+//   AX  x-sums of alpha, beta, gamma over the TX output columns.
+//   AYs y-sums of the three over the TY output rows.
+//   AZ  (registers) one lane per output column: a k-deep ring of the xy-sums -> z-sums
 //       box(alpha), box(beta), box(gamma), combined with p,t of the output plane (re-read from
 //       the L2 as their last use, non-temporal) into the gradient, the only per-voxel write to HBM.
+//
+// Every box-sum is a sum of its window's own values (lncc_window.h): in x and y blocks of k
+// values give each window as a block suffix plus the next block's prefix; along D the march is
+// unrolled by k, the ring slot r of plane zi is its position in its block of k planes, and the
+// z-sum at zi is the prefix of the current block (planes of slots 0..r, carried in registers)
+// plus the suffix of the previous block still in the ring (slots r+1..k-1). So windows of zeros
+// sum to exactly zero and windows of one constant to exactly k^3 c, as the reference's direct
+// sums do; running sums (add the entering value, subtract the leaving one) would carry the
+// rounding of every earlier plane into them.
 //
 // Software pipeline: the chain F -> X -> Y -> AX -> AYs -> AZ alternates between two phases per
 // plane, P0 = {F(zi), Y(zi-1), AYs(zi-2)} and P1 = {X(zi), AX(zi-1), AZ(zi-2)}, so each plane costs
 // two workgroup barriers, and the stages that share a phase run on disjoint waves.
 //
-// MODE_DUAL adds the gradient with respect to target (not in the reference): the loss is symmetric
-// in p and t, so Y also forms alpha and beta with the roles of p and t swapped, and AX, AYs and AZ
-// carry five fields (gamma is shared).
-//
 // Reference semantics (fused_lncc/csrc/lncc3d.cu:93-107, baselines/torch_lncc.py:25-32):
 //   cross = Spt - Sp St/n ; vp = max(Spp - Sp^2/n, 0) + dr ; vt likewise ; ncc = cross^2/(vp vt);
 //   ncc >= 1 -> ncc = 1 and zero adjoints; NaN keeps NaN ncc and zero adjoints;
 //   A = dncc/dSp, Bc = dncc/dvp, Cc = dncc/dcross; grad = -(1/M)(box A + 2p box Bc + t box Cc).
-// With r = 1/(vp vt), cr = cross r, u = cr vt, w = St - Sp u the kernel carries
-//   alpha = cr w, beta = cr u, gamma = cr   (A = -2 alpha/n, Bc = -beta, Cc = 2 gamma)
-// so that grad = (2/M) (box(alpha)/n + p box(beta) - t box(gamma)).
+// The kernel forms the n-fold quantities X = n Spt - Sp St, VP = max(n Spp - Sp^2, 0) + n dr and
+// VT likewise (ncc = X^2/(VP VT)): an integer n times a sum and one fused multiply-add, so a
+// window of one constant c gives exactly X = 0 and VP - n dr = 0 whenever n^2 c^2 is a float, as
+// the reference's Sp St / n division does (a reciprocal 1/n would leave a residue there that the
+// division by dr^2 blows up). With r = 1/(VP VT), c = X r, u = c VT, w = St - Sp u it carries
+//   alpha = c w, beta = c u, gamma = c   (A = -2 alpha, Bc = -n beta, Cc = 2 n gamma)
+// so that grad = (2n/M) (box(alpha)/n + p box(beta) - t box(gamma)).
 #pragma once
 #include "lncc_common.h"
 #include "lncc_launch.h"
+#include "lncc_window.h"
 
 namespace fl {
 
@@ -54,28 +62,10 @@ __device__ __forceinline__ void lds_row(const float* __restrict__ src, float (&v
     }
 }
 
-// Running window sums of width 2H+1: out[i] = v[i] + ... + v[i+2H] for i < S.
-template <int H, int S>
-__device__ __forceinline__ void window_sums(const float (&v)[S + 2 * H], float (&out)[S]) {
-    float acc = v[0];
-#pragma unroll
-    for (int i = 1; i <= 2 * H; ++i) acc += v[i];
-    out[0] = acc;
-#pragma unroll
-    for (int i = 1; i < S; ++i) {
-        acc += v[i + 2 * H] - v[i - 1];
-        out[i] = acc;
-    }
-}
-
 template <int HH, bool BF16, int MODE>
 __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) {
-    // DUAL: the target gradient too, from two more adjoint fields (the loss is symmetric in p and
-    // t, so they are alpha and beta with the roles of p and t swapped; gamma is shared)
-    constexpr bool DUAL = (MODE == MODE_DUAL);
-    constexpr bool ADJ = (MODE == MODE_GRAD) || DUAL;
-    constexpr int NA = DUAL ? 5 : 3;
-    using G = Geo<HH, NA>;
+    constexpr bool ADJ = (MODE == MODE_GRAD);
+    using G = Geo<HH>;
     constexpr int K = G::K;
     constexpr int ELEM = BF16 ? 2 : 4;
     constexpr int J = G::J;
@@ -85,9 +75,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // alias the writes of another and can overlap them
     __shared__ __align__(16) float Zs[5 * G::ZP + G::PAD];
     __shared__ __align__(16) float Xs[5 * G::XP + G::PAD];
-    __shared__ __align__(16) float Gs[ADJ ? NA * G::GP + G::PAD : 4];
-    __shared__ __align__(16) float GXs[ADJ ? NA * G::GXP + G::PAD : 4];
-    __shared__ __align__(16) float GY[ADJ ? NA * G::GYP : 2];
+    __shared__ __align__(16) float Gs[ADJ ? 3 * G::GP + G::PAD : 4];
+    __shared__ __align__(16) float GXs[ADJ ? 3 * G::GXP + G::PAD : 4];
+    __shared__ __align__(16) float GY[ADJ ? 3 * G::GYP : 2];
     __shared__ double red[NT / 64];
 
     const int tid = threadIdx.x;
@@ -110,7 +100,6 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const char* pvol = (const char*)a.pred + b * D * HW * ELEM;
     const char* tvol = (const char*)a.target + b * D * HW * ELEM;
     char* const gvol = ADJ ? (char*)a.grad + b * D * HW * ELEM : nullptr;
-    char* const tgvol = DUAL ? (char*)a.tgrad + b * D * HW * ELEM : nullptr;
 
     // ---- F: per-lane input columns
     uint32_t voff[J];
@@ -130,7 +119,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     int u_src[G::U1], u_dst[G::U1], u_kind[G::U1];
 #pragma unroll
     for (int k = 0; k < G::U1; ++k) u_kind[k] = p1_unit<G, ADJ>(tid + k * NT, u_src[k], u_dst[k]);
-    // P0: Y items on lanes [0, YITEMS), AYs units on waves 10, 11, 14, 15 (and 6 with five fields)
+    // P0: Y items on lanes [0, YITEMS), AYs units on waves 10, 11, 14, 15
     const bool has_y = tid < G::YITEMS;
     int y_seg = 0, y_ax = 0;  // rows seg of AX positions
     if (has_y) y_item<G>(tid, y_seg, y_ax);
@@ -153,7 +142,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const bool has_b = ays_unit<G>(tid, b_src, b_dst) && ADJ;
     const bool has_z = ADJ && tid < G::NOUT;
     int z_ox, z_oy;
-    az_lane(tid, z_ox, z_oy);
+    az_lane<G>(tid, z_ox, z_oy);
     const bool z_in = has_z && x0 + z_ox < Wd && y0 + z_oy < Hd;
     const uint32_t z_voff = z_in ? (uint32_t)(((y0 + z_oy) * Wd + x0 + z_ox) * ELEM) : kOOB;
 
@@ -163,26 +152,24 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const int zc_lo = ADJ ? max(z0 - HH, 0) : z0;
     const int zc_hi = ADJ ? min(z1 + HH, D) : z1;
 
-    // F state: running z-sums; p,t of the next plane (prefetched one step ahead); the plane leaving
-    // the window comes from a k-deep register ring of the last k planes' p,t (k <= 7) or, where
-    // the ring would not fit in the register budget, is re-read from global memory (still cache
-    // resident) and prefetched like the new plane: at k = 9, and in the five-field mode, which
-    // spends those registers on its two extra z-rings of xy-sums
-    constexpr bool RING = K <= 7 && !DUAL;
-    constexpr int KR = RING ? K : 1;
-    float zsum[J][5], pnext[J], tnext[J], pring[KR][J], tring[KR][J], pold[J], told[J];
+    // F state: the ring of the last k planes' p,t (slot r = position of the plane in its block of
+    // k), the prefix sums of the five fields over the current block, and p,t of the next plane
+    // (prefetched one step ahead). The ring starts at zero: nothing before the first plane of the
+    // march enters a window that is used.
+    float pring[J][K], tring[J][K], fpre[J][5], zsum[J][5], pnext[J], tnext[J];
     float pz = 0.f, tzz = 0.f;  // AZ: p,t at this step's output plane (prefetched one step ahead)
 #pragma unroll
     for (int j = 0; j < J; ++j) {
 #pragma unroll
-        for (int q = 0; q < 5; ++q) zsum[j][q] = 0.f;
-#pragma unroll
-        for (int r = 0; r < KR; ++r) {
-            pring[r][j] = 0.f;
-            tring[r][j] = 0.f;
+        for (int q = 0; q < 5; ++q) {
+            fpre[j][q] = 0.f;
+            zsum[j][q] = 0.f;
         }
-        pold[j] = 0.f;
-        told[j] = 0.f;
+#pragma unroll
+        for (int r = 0; r < K; ++r) {
+            pring[j][r] = 0.f;
+            tring[j][r] = 0.f;
+        }
     }
     {
         const __amdgpu_buffer_rsrc_t rp = make_rsrc(pvol + (int64_t)zlo * HW * ELEM, plane_bytes);
@@ -193,26 +180,27 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             tnext[j] = load_elem<BF16>(rt, voff[j]);
         }
     }
-    float gring[NA][K], gz[NA];
+    // AZ state: the ring of the last k planes' xy-sums of alpha, beta, gamma and their prefix sums
+    // over the current block
+    float gring[3][K], gpre[3];
 #pragma unroll
-    for (int c = 0; c < NA; ++c) {
-        gz[c] = 0.f;
+    for (int c = 0; c < 3; ++c) {
+        gpre[c] = 0.f;
 #pragma unroll
         for (int r = 0; r < K; ++r) gring[c][r] = 0.f;
     }
 
     double loss_acc = 0.0;
-    const float inv_n = a.inv_n, dr = a.dr;
+    const float inv_n = a.inv_n, nf = a.nf, ndr = a.ndr;
 
     // Plane addresses advance by one plane per step: zoff = zi * plane size, and every plane the
     // loop touches sits at a fixed plane distance from zi. A plane outside its valid range gets a
     // zero-sized resource (its address is never dereferenced).
     const uint64_t PB = (uint64_t)HW * ELEM;
     const uint64_t pva = (uint64_t)(uintptr_t)pvol, tva = (uint64_t)(uintptr_t)tvol;
-    const uint64_t gva = (uint64_t)(uintptr_t)gvol, tgva = (uint64_t)(uintptr_t)tgvol;
+    const uint64_t gva = (uint64_t)(uintptr_t)gvol;
     uint64_t zoff = (uint64_t)zlo * PB;
     const int zn_hi = min(zhi, D);                 // F: new plane zi+1 valid while zi+1 < zn_hi
-    const int zq_lo = zlo + K - 1, zq_hi = min(D + K - 1, zhi - 1);  // old plane zi+1-K: zi in [zq_lo, zq_hi)
     constexpr int ZO = 2 + 2 * HH;                 // AZ: output plane zi-ZO
 
     // Stage bodies; the march below orders them per phase.
@@ -226,76 +214,53 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
         for (int i = 0; i < G::SY; ++i) {
             const int ay = y_start + i;
             const float Sp = S[0][i], St = S[1][i], Spp = S[2][i], Stt = S[3][i], Spt = S[4][i];
-            const float mp = Sp * inv_n, mt = St * inv_n;
-            const float cross = fmaf(-mp, St, Spt);
-            const float vp = fmaxf(fmaf(-mp, Sp, Spp), 0.f) + dr;
-            const float vt = fmaxf(fmaf(-mt, St, Stt), 0.f) + dr;
-            const float rr = __builtin_amdgcn_rcpf(vp * vt);
-            const float cr = cross * rr;
-            const float ncc = cross * cr;
+            const float X = fmaf(-Sp, St, nf * Spt);
+            const float VP = fmaxf(fmaf(-Sp, Sp, nf * Spp), 0.f) + ndr;
+            const float VT = fmaxf(fmaf(-St, St, nf * Stt), 0.f) + ndr;
+            const float rr = __builtin_amdgcn_rcpf(VP * VT);
+            const float cr = X * rr;
+            const float ncc = X * cr;
             const bool live = y_inv[i] && (ncc < 1.0f);
             const float nccc = (ncc >= 1.0f) ? 1.0f : ncc;
             if (count && y_core[i]) lsum += nccc;
             if constexpr (ADJ) {
                 // masking cr masks all three coefficients (alpha, beta, gamma are multiples of it)
                 const float crm = live ? cr : 0.f;
-                const float uu = crm * vt;
+                const float uu = crm * VT;
                 const float w = fmaf(-Sp, uu, St);
                 Gs[0 * G::GP + ay * G::GS + y_ax] = crm * w;
                 Gs[1 * G::GP + ay * G::GS + y_ax] = crm * uu;
                 Gs[2 * G::GP + ay * G::GS + y_ax] = crm;
-                if constexpr (DUAL) {  // the same with p and t swapped
-                    const float ut = crm * vp;
-                    const float wt = fmaf(-St, ut, Sp);
-                    Gs[3 * G::GP + ay * G::GS + y_ax] = crm * wt;
-                    Gs[4 * G::GP + ay * G::GS + y_ax] = crm * ut;
-                }
             }
             if constexpr (MODE == MODE_MAPS) {
                 if (count && y_core[i]) {
-                    const float uu = cr * vt;
+                    const float uu = cr * VT;
                     const float w = fmaf(-Sp, uu, St);
                     const int gx = x0 - HH + y_ax, gy = y0 - HH + ay;
                     const int64_t o = ((b * D + zcY) * Hd + gy) * (int64_t)Wd + gx;
                     a.ncc_map[o] = nccc;
                     if (a.a_map) {  // null: the ncc map alone
-                        a.a_map[o] = live ? -2.f * inv_n * (cr * w) : 0.f;
-                        a.b_map[o] = live ? -(cr * uu) : 0.f;
-                        a.c_map[o] = live ? 2.f * cr : 0.f;
+                        a.a_map[o] = live ? -2.f * (cr * w) : 0.f;
+                        a.b_map[o] = live ? -nf * (cr * uu) : 0.f;
+                        a.c_map[o] = live ? (2.f * nf) * cr : 0.f;
                     }
                 }
             }
         }
         loss_acc += (double)lsum;
     };
-    // F(zi): z-sums of the input region. Consume the planes prefetched one step ago, then prefetch
-    // the next ones. Every global access of the loop is issued unconditionally (inactive ones
-    // through a zero-sized buffer), so the number of outstanding memory operations is the same on
-    // every path and the waits before use stay exact. With STORE the z-sums go to the LDS column
-    // by column as they are formed; without, f_store writes them later.
+    // F(zi): z-sums of the input region over planes [zi-k+1, zi] (zstep5: the plane prefetched one
+    // step ago joins the block prefix and the ring, the previous block's suffix comes from the
+    // ring), then the prefetch of the next plane. Every global access of the loop is issued unconditionally
+    // (inactive ones through a zero-sized buffer), so the number of outstanding memory operations
+    // is the same on every path and the waits before use stay exact. With STORE the z-sums go to
+    // the LDS column by column as they are formed; without, f_store writes them later.
     auto f_sums = [&](auto rc, auto store, int zi, uint64_t zoff) __attribute__((always_inline)) {
         constexpr int r = decltype(rc)::value;
         constexpr bool STORE = decltype(store)::value;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            // plane zi replaces plane zi-k (ring slot r; the ring starts at zero: nothing before
-            // the first plane of the march was added)
-            const float p = pnext[j], t = tnext[j];
-            float po, to;
-            if constexpr (RING) {
-                po = pring[r][j];
-                to = tring[r][j];
-                pring[r][j] = p;
-                tring[r][j] = t;
-            } else {
-                po = pold[j];
-                to = told[j];
-            }
-            zsum[j][0] += p - po;
-            zsum[j][1] += t - to;
-            zsum[j][2] = fmaf(p, p, fmaf(-po, po, zsum[j][2]));
-            zsum[j][3] = fmaf(t, t, fmaf(-to, to, zsum[j][3]));
-            zsum[j][4] = fmaf(p, t, fmaf(-po, to, zsum[j][4]));
+            zstep5<K, r>(pnext[j], tnext[j], fpre[j], pring[j], tring[j], zsum[j]);
             if constexpr (STORE) {
                 if (zaddr[j] >= 0) {
 #pragma unroll
@@ -303,7 +268,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 }
             }
         }
-        // prefetch plane zi+1 (and, without the ring, plane zi+1-k leaving the window)
+        // prefetch plane zi+1
         const bool okn = zi + 1 < zn_hi;
         const __amdgpu_buffer_rsrc_t rpn = rsrc_at(pva + zoff + PB, plane_bytes, okn);
         const __amdgpu_buffer_rsrc_t rtn = rsrc_at(tva + zoff + PB, plane_bytes, okn);
@@ -311,19 +276,6 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
         for (int j = 0; j < J; ++j) {
             pnext[j] = load_elem<BF16>(rpn, voff[j]);
             tnext[j] = load_elem<BF16>(rtn, voff[j]);
-        }
-        if constexpr (!RING) {
-            // non-temporal: the last use of the halo columns' lines in this tile (the central ones
-            // are re-read once more by AZ two steps later); marked evict-first they leave the L2
-            // to the planes that are still to be re-read
-            const bool okq = zi >= zq_lo && zi < zq_hi;
-            const __amdgpu_buffer_rsrc_t rpq = rsrc_at(pva + zoff - (K - 1) * PB, plane_bytes, okq);
-            const __amdgpu_buffer_rsrc_t rtq = rsrc_at(tva + zoff - (K - 1) * PB, plane_bytes, okq);
-#pragma unroll
-            for (int j = 0; j < J; ++j) {
-                pold[j] = load_elem<BF16, kNT>(rpq, voff[j]);
-                told[j] = load_elem<BF16, kNT>(rtq, voff[j]);
-            }
         }
     };
     auto f_store = [&]() __attribute__((always_inline)) {
@@ -336,53 +288,34 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
         }
     };
     // X(zi) or AX(zi-1), the lane's unit: x-sums of one z-sum (feeds Y at the next plane) or of
-    // one of alpha, beta, gamma at plane zcY, over one segment. Either in one piece (u_whole), or
-    // with the row read early and the sums formed by u_math later; the early read takes SX + 2h
-    // floats for both kinds (SX >= SA), and an AX row's extra floats stay inside Gs, unused.
+    // one of alpha, beta, gamma at plane zcY, over one segment. The row is read early and the sums
+    // formed by u_math later; the early read takes SX + 2h floats for both kinds (SX >= SA), and an
+    // AX row's extra floats stay inside Gs, unused.
     static_assert(G::U1 == 1 && G::SX >= G::SA, "one unit per lane");
-    auto u_whole = [&](bool runX, bool runA) __attribute__((always_inline)) {
-        if (runX) {
-            float v[G::SX + 2 * HH], o[G::SX];
-            lds_row(Zs + u_src[0], v);
-            window_sums<HH, G::SX>(v, o);
-#pragma unroll
-            for (int i = 0; i < G::SX; ++i) Xs[u_dst[0] + i * G::XS] = o[i];
-        } else if (runA) {
-            float v[G::SA + 2 * HH], o[G::SA];
-            lds_row(Gs + u_src[0], v);
-            window_sums<HH, G::SA>(v, o);
-#pragma unroll
-            for (int i = 0; i < G::SA; ++i) GXs[u_dst[0] + i * G::GXS] = o[i];
-        }
-    };
     auto u_math = [&](const float (&uv)[G::SX + 2 * HH], bool runX, bool runA) __attribute__((always_inline)) {
         if (runX) {
             float o[G::SX];
-            window_sums<HH, G::SX>(uv, o);
+            box_sums<HH, G::SX>(uv, o);
 #pragma unroll
             for (int i = 0; i < G::SX; ++i) Xs[u_dst[0] + i * G::XS] = o[i];
         } else if (runA) {
             float v[G::SA + 2 * HH], o[G::SA];
 #pragma unroll
             for (int i = 0; i < G::SA + 2 * HH; ++i) v[i] = uv[i];
-            window_sums<HH, G::SA>(v, o);
+            box_sums<HH, G::SA>(v, o);
 #pragma unroll
             for (int i = 0; i < G::SA; ++i) GXs[u_dst[0] + i * G::GXS] = o[i];
         }
     };
 
     // Stage order inside a phase. Each wave runs its stages in program order, so a stage placed
-    // between the issue of another stage's LDS reads and their use hides part of their latency.
-    // Measured at (2,16,128^3):
-    //  * P0, k <= 5, one gradient: Y's rows, then F's arithmetic and prefetch, then Y's math, AYs
-    //    and F's stores (k = 5: -7%). At k >= 7 the rows held across F exceed the 128-register
-    //    budget of a 1024-lane workgroup (spills), and with both gradients the reorder measured
-    //    slower (k = 3: +12%): there F stays last.
-    //  * P1: AZ's xy-sums are read before everything else (-2%), and the unit's row is read
-    //    before AZ and its sums formed after AZ. With both gradients at k <= 5 the plain order
-    //    (the unit, then AZ with its reads) measured 4% faster and is kept there.
-    constexpr bool F_EARLY = HH <= 2 && !DUAL;
-    constexpr bool P1_PLAIN = HH <= 2 && DUAL;
+    // between the issue of another stage's LDS reads and their use hides part of their latency:
+    //  * P0, k <= 5: Y's rows, then F's arithmetic and prefetch, then Y's math, AYs and F's stores.
+    //    At k >= 7 the rows held across F exceed the 128-register budget of a 1024-lane workgroup
+    //    (spills): there F runs last.
+    //  * P1: AZ's xy-sums are read before everything else, and the unit's row is read before AZ
+    //    and its sums formed after AZ.
+    constexpr bool F_EARLY = HH <= 2;
 
     for (int base = zlo; base < zhi; base += K) {
         static_for<0, K>([&](auto rc) __attribute__((always_inline)) {
@@ -405,7 +338,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 if (actY && has_y) {
                     float S[5][G::SY];
 #pragma unroll
-                    for (int q = 0; q < 5; ++q) window_sums<HH, G::SY>(yv[q], S[q]);
+                    for (int q = 0; q < 5; ++q) box_sums<HH, G::SY>(yv[q], S[q]);
                     y_math(S, zcY);
                 }
             } else if (actY && has_y) {
@@ -415,7 +348,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 for (int q = 0; q < 5; ++q) {
                     float yv[G::SY + 2 * HH];
                     lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv);
-                    window_sums<HH, G::SY>(yv, S[q]);
+                    box_sums<HH, G::SY>(yv, S[q]);
                 }
                 y_math(S, zcY);
             }
@@ -424,7 +357,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 if (actB && has_b) {
                     float v[G::SB + 2 * HH], o[G::SB];
                     lds_row(GXs + b_src, v);
-                    window_sums<HH, G::SB>(v, o);
+                    box_sums<HH, G::SB>(v, o);
 #pragma unroll
                     for (int i = 0; i < G::SB; ++i) GY[b_dst + i * G::GYS] = o[i];
                 }
@@ -438,33 +371,27 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 
             // ============================ phase P1 ============================
             // X(zi) and AX(zi-1) on the unit lanes, AZ(zi-2) on the output lanes
-            float ys[NA];
-            auto read_ys = [&]() __attribute__((always_inline)) {
+            float ys[3];
+            if constexpr (ADJ) {
 #pragma unroll
-                for (int c = 0; c < NA; ++c) ys[c] = actB ? GY[c * G::GYP + z_oy * G::GYS + z_ox] : 0.f;
-            };
-            if constexpr (ADJ && !P1_PLAIN) read_ys();
+                for (int c = 0; c < 3; ++c) ys[c] = actB ? GY[c * G::GYP + z_oy * G::GYS + z_ox] : 0.f;
+            }
             const int zcX = zi - HH;
             const bool actX = zcX >= zc_lo && zcX < zc_hi;
             const bool runX = u_kind[0] == 1 && actX, runA = ADJ && u_kind[0] == 2 && actY;
             float uv[G::SX + 2 * HH];
-            if constexpr (P1_PLAIN) {
-                u_whole(runX, runA);
-            } else if (runX || runA) {
-                lds_row((runA ? Gs : Zs) + u_src[0], uv);
-            }
+            if (runX || runA) lds_row((runA ? Gs : Zs) + u_src[0], uv);
             if constexpr (ADJ) {
-                // AZ(zi-2): z ring of the xy-sums, combine at the output plane zo (lanes without an
-                // output column run on a clamped one and store out of range, i.e. nothing)
+                // AZ(zi-2): z-sums of the xy-sums over the k planes of the output plane zo = the
+                // prefix of the current block plus the previous block's suffix still in the ring
+                // (lanes without an output column run on a clamped one and store out of range,
+                // i.e. nothing)
                 constexpr int r = decltype(rc)::value;
-                if constexpr (P1_PLAIN) read_ys();
+                float gw[3];
 #pragma unroll
-                for (int c = 0; c < NA; ++c) {
-                    gz[c] += ys[c] - gring[c][r];
-                    gring[c][r] = ys[c];
-                }
+                for (int c = 0; c < 3; ++c) gw[c] = zstep1<K, r>(ys[c], gpre[c], gring[c]);
                 const int zo = zi - ZO;
-                const float g = a.gscale * fmaf(inv_n, gz[0], fmaf(pz, gz[1], -tzz * gz[2]));
+                const float g = a.gscale * fmaf(inv_n, gw[0], fmaf(pz, gw[1], -tzz * gw[2]));
                 // Non-temporal: the gradient is never read back, and this re-read of p,t is the
                 // last use of those lines. With the default policy both would be promoted in the
                 // L2 and push out the planes that F loaded and this stage re-reads 2h+2 steps
@@ -474,17 +401,13 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 // those stores keep the default policy, so that the L2 merges the two halves into
                 // one write.
                 store_elem_buf<BF16, BF16 ? 0 : kNT>(rsrc_at(gva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, g);
-                if constexpr (DUAL) {
-                    const float gt = a.gscale * fmaf(inv_n, gz[3], fmaf(tzz, gz[4], -pz * gz[2]));
-                    store_elem_buf<BF16, BF16 ? 0 : kNT>(rsrc_at(tgva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, gt);
-                }
                 // prefetch p,t at the next step's output plane; issued after this step's use, so
                 // one register each suffices and no copy has to wait for the load
                 const bool oko = zo + 1 >= z0 && zo + 1 < z1;
                 pz = load_elem<BF16, kNT>(rsrc_at(pva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
                 tzz = load_elem<BF16, kNT>(rsrc_at(tva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
             }
-            if constexpr (!P1_PLAIN) u_math(uv, runX, runA);
+            u_math(uv, runX, runA);
             zoff += PB;
             __syncthreads();
         });
@@ -514,13 +437,6 @@ hipError_t launch_fused(int mode, bool bf16, const FusedArgs& a, uint32_t nblock
         if (bf16) FL_LAUNCH(true, MODE_GRAD); else FL_LAUNCH(false, MODE_GRAD);
     } else if (mode == MODE_MAPS) {
         if (bf16) FL_LAUNCH(true, MODE_MAPS); else FL_LAUNCH(false, MODE_MAPS);
-    } else if (mode == MODE_DUAL) {
-        // five adjoint fields fit in LDS for k <= 7 only; k = 9 takes two MODE_GRAD passes
-        if constexpr (HH <= 3) {
-            if (bf16) FL_LAUNCH(true, MODE_DUAL); else FL_LAUNCH(false, MODE_DUAL);
-        } else {
-            return hipErrorInvalidValue;
-        }
     } else {
         return hipErrorInvalidValue;
     }

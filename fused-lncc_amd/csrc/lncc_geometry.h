@@ -11,12 +11,15 @@
 
 namespace fl {
 
-// Workgroup: 1024 lanes (16 wave64s, one workgroup per CU). Output tile: TX x TY columns of one
-// volume, marched along D.
+// Workgroup: 1024 lanes (16 wave64s, one workgroup per CU). Output tile: TX x tile_rows(H)
+// columns of one volume, marched along D. The tile is 32 x 32 for k <= 7 and 32 x 24 for k = 9,
+// whose input region (48 x 40 columns) then still takes two columns per lane, so that the
+// register ring of the last k planes fits (32 x 32 at k = 9 would need three).
 constexpr int NT = 1024;
 constexpr int WG_PER_CU = 1;
 constexpr int TX = 32;
-constexpr int TY = 32;
+constexpr int TY_MAX = 32;
+FL_HD constexpr int tile_rows(int halo) { return halo >= 4 ? 24 : 32; }
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
@@ -32,17 +35,15 @@ constexpr int rup64(int n) { return (n + 63) / 64 * 64; }
 //   input region   ix in [0,IX), iy in [0,IY)  <-> global (x0-2H+ix, y0-2H+iy)
 //   adjoint region ax in [0,AX), ay in [0,AY)  <-> global (x0-H+ax,  y0-H+ay)
 //   output tile    ox in [0,TX), oy in [0,TY)  <-> global (x0+ox,    y0+oy)
-// Running-sum passes work on segments of S consecutive outputs. The X and Y passes round their
+// The box-sum passes work on segments of S consecutive outputs. The X and Y passes round their
 // output range up to whole segments: the extra outputs read row padding and land in padding rows
 // of the destination that no later pass reads (and that the loss never counts), so no lane needs
-// a per-output store mask.
-// NA = number of adjoint fields carried from Y to AZ: 3 (alpha, beta, gamma of the pred gradient)
-// or 5 (with alpha', beta' of the target gradient; gamma is shared)
-template <int H, int NA = 3>
+// a per-output store mask. Three adjoint fields (alpha, beta, gamma) go from Y to AZ.
+template <int H>
 struct Geo {
-    static constexpr int HALO = H, NADJ = NA;
+    static constexpr int HALO = H, NADJ = 3;
     static constexpr int K = 2 * H + 1;
-    static constexpr int TY = fl::TY;
+    static constexpr int TY = tile_rows(H);
     static constexpr int IX = TX + 4 * H, IY = TY + 4 * H;
     static constexpr int AX = TX + 2 * H, AY = TY + 2 * H;
     static constexpr int NIN = IX * IY;
@@ -56,23 +57,22 @@ struct Geo {
     static constexpr int SA = 16, ASEG = TX / SA, AITEMS = AY * ASEG;
     // AYs: y-sums of the three; items (ox, seg), outputs oy < TY
     static constexpr int SB = TY / 2, BSEG = TY / SB, BITEMS = TX * BSEG;
-    // Work units of the running-sum passes are single quantities of one segment. Waves are
-    // spread over the 4 SIMDs of the CU round-robin (wave w on SIMD w % 4), so the heavy items
-    // are placed to even out each SIMD's share of a phase: in phase P1 the X units (5 per item)
-    // fill the first waves and the AX units (3 per item) start on the next wave boundary; in
-    // phase P0 the Y items fill the first waves (SIMDs 0 and 1 get the extra ones) and the AYs
-    // units (3 per item) go to waves 10, 11, 14, 15 (SIMDs 2 and 3), B_PER_WAVE each.
-    // With five adjoint fields the AYs units (two rows of 32 per field) take five whole waves.
-    static constexpr int UX = 5 * XITEMS, UA = NA * AITEMS, AX_LANE0 = rup64(UX), U1 = 1;
-    static constexpr int UB = NA * BITEMS, B_PER_WAVE = NA == 3 ? UB / 4 : 64;
-    static_assert(YITEMS <= 10 * 64 && AX_LANE0 + UA <= NT && BSEG == 2 && TX == 32 &&
-                      (NA == 3 ? (UB == 192 && B_PER_WAVE == 48) : (NA == 5 && UB == 320)),
+    // Work units of the box-sum passes are single quantities of one segment. Waves are spread
+    // over the 4 SIMDs of the CU round-robin (wave w on SIMD w % 4), so the heavy items are placed
+    // to even out each SIMD's share of a phase: in phase P1 the X units (5 per item) fill the
+    // first waves and the AX units (3 per item) start on the next wave boundary; in phase P0 the
+    // Y items fill the first waves (SIMDs 0 and 1 get the extra ones) and the AYs units (3 per
+    // item) go to waves 10, 11, 14, 15 (SIMDs 2 and 3), B_PER_WAVE each.
+    static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, AX_LANE0 = rup64(UX), U1 = 1;
+    static constexpr int UB = 3 * BITEMS, B_PER_WAVE = UB / 4;
+    static_assert(YITEMS <= 10 * 64 && AX_LANE0 + UA <= NT && BSEG == 2 && TX == 32 && UB == 192 &&
+                      B_PER_WAVE == 48 && NIN <= 2 * NT && TY <= TY_MAX,
                   "lanes");
     // every segment starts on a 16-byte boundary (rows are read as float4)
     static_assert(XR >= AX && TX % SA == 0 && TY % SB == 0 && SX % 4 == 0 && SY % 4 == 0 &&
                       SA % 4 == 0 && SB % 4 == 0, "segments");
-    // LDS layout (floats): Zs[5][IY][ZS], XsT[5][XR][XS] (transposed), Gs[NA][YR][GS],
-    // GXsT[NA][TX][GXS] (transposed), GY[NA][TY][GYS]; each buffer but GY ends in PAD spare floats
+    // LDS layout (floats): Zs[5][IY][ZS], XsT[5][XR][XS] (transposed), Gs[3][YR][GS],
+    // GXsT[3][TX][GXS] (transposed), GY[3][TY][GYS]; each buffer but GY ends in PAD spare floats
     static constexpr int ZS = stride4(IX), XS = stride4(cmax(IY, AY)), GS = stride4(AX), GXS = XS;
     static constexpr int GYS = TX + 1, PAD = 16;
     static constexpr int ZP = IY * ZS, XP = XR * XS, GP = YR * GS, GXP = TX * GXS, GYP = TY * GYS;
@@ -81,7 +81,7 @@ struct Geo {
     static_assert(SX + rup4(SX + 2 * H) <= ZS + PAD && YR - SY + rup4(SY + 2 * H) <= XS + PAD &&
                       TX - SA + rup4(SA + 2 * H) <= GS + PAD && TY - SB + rup4(SB + 2 * H) <= GXS + PAD,
                   "row reads");
-    static constexpr int LDS_FLOATS = 5 * (ZP + XP) + NA * (GP + GXP + GYP) + 4 * PAD;
+    static constexpr int LDS_FLOATS = 5 * (ZP + XP) + 3 * (GP + GXP + GYP) + 4 * PAD;
     static_assert(LDS_FLOATS * 4 <= 160 * 1024, "LDS");
 };
 
@@ -151,27 +151,20 @@ FL_HD inline void y_item(int tid, int& seg, int& ax) {
     split32<G::AX>(tid, G::YSEG, seg, ax);
 }
 
-// AYs unit of lane tid, on waves 10, 11, 14, 15 (and 6 with five fields), B_PER_WAVE lanes each:
-// y-sums of one adjoint field over one segment of output column ox; reads GXs from src, writes GY
-// at dst + i * GYS. Returns false for lanes without a unit.
+// AYs unit of lane tid, on waves 10, 11, 14, 15, B_PER_WAVE lanes each: y-sums of one adjoint
+// field over one segment of output column ox; reads GXs from src, writes GY at dst + i * GYS.
+// Returns false for lanes without a unit.
 template <class G>
 FL_HD inline bool ays_unit(int tid, int& src, int& dst) {
-    constexpr bool five = G::NADJ == 5;
     src = 0;
     dst = 0;
     const int wave = tid >> 6, l = tid & 63;
-    const int bslot = wave == 10 ? 0 : wave == 11 ? 1 : wave == 14 ? 2 : wave == 15 ? 3 : (five && wave == 6) ? 4 : -1;
+    const int bslot = wave == 10 ? 0 : wave == 11 ? 1 : wave == 14 ? 2 : wave == 15 ? 3 : -1;
     if (bslot < 0 || l >= G::B_PER_WAVE) return false;
-    // rows (c, seg) of TX = 32 positions. Three fields: slot s takes row s on its first 32 lanes
-    // and half of row 4 + s/2 on the next 16. Five fields: slot s takes both rows of field s.
-    int row, ox;
-    if constexpr (five) {
-        row = 2 * bslot + (l >> 5);
-        ox = l & 31;
-    } else {
-        row = l < 32 ? bslot : 4 + (bslot >> 1);
-        ox = l < 32 ? l : (bslot & 1) * 16 + (l - 32);
-    }
+    // rows (c, seg) of TX = 32 positions: slot s takes row s on its first 32 lanes and half of
+    // row 4 + s/2 on the next 16
+    const int row = l < 32 ? bslot : 4 + (bslot >> 1);
+    const int ox = l < 32 ? l : (bslot & 1) * 16 + (l - 32);
     const int c = row / G::BSEG, start = (row % G::BSEG) * G::SB;
     src = c * G::GXP + ox * G::GXS + start;
     dst = c * G::GYP + start * G::GYS + ox;
@@ -180,9 +173,10 @@ FL_HD inline bool ays_unit(int tid, int& src, int& dst) {
 
 // AZ: output column (ox, oy) of lane tid (lanes beyond the tile run on a clamped row); it reads
 // GY at c * GYP + oy * GYS + ox.
+template <class G>
 FL_HD inline void az_lane(int tid, int& ox, int& oy) {
     ox = tid % TX;
-    oy = tid / TX < TY - 1 ? tid / TX : TY - 1;
+    oy = tid / TX < G::TY - 1 ? tid / TX : G::TY - 1;
 }
 
 }  // namespace fl

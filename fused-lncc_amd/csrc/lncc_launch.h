@@ -5,14 +5,12 @@
 
 namespace fl {
 
-// MODE_DUAL: the gradients with respect to pred and to target in one pass (k <= 7)
-enum Mode { MODE_LOSS = 0, MODE_GRAD = 1, MODE_MAPS = 2, MODE_DUAL = 3 };
+enum Mode { MODE_LOSS = 0, MODE_GRAD = 1, MODE_MAPS = 2 };
 
 struct FusedArgs {
     const void* pred;
     const void* target;
-    void* grad;       // MODE_GRAD, MODE_DUAL: gradient wrt pred, pred dtype
-    void* tgrad;      // MODE_DUAL: gradient wrt target, target dtype
+    void* grad;       // MODE_GRAD: gradient wrt pred, pred dtype
     float* ncc_map;   // MODE_MAPS: fp32 maps ncc, A, Bc, Cc (reference definitions)
     float* a_map;
     float* b_map;
@@ -20,7 +18,8 @@ struct FusedArgs {
     double* partials; // one ncc partial sum per workgroup
     int dimD, dimH, dimW;
     int ntx, nty, nzc, dchunk;
-    float inv_n, dr, gscale;  // gscale = 2/M
+    float inv_n, nf, ndr;     // 1/n, n = k^3 and n * smooth_dr as float32
+    float gscale;             // 2 n / M
 };
 
 struct BoxArgs {
@@ -40,7 +39,9 @@ hipError_t launch_fused_h2(int mode, bool bf16, const FusedArgs& a, uint32_t nbl
 hipError_t launch_fused_h3(int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
 hipError_t launch_fused_h4(int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
 
-// box3d (nfields = 1, fp32 out) and the reference backward combine (nfields = 3)
+// box3d (nfields = 1, fp32 out) and the reference backward combine (nfields = 3): workgroups of
+// kBoxLanes lanes, one per 16 x 16 tile of one volume
+constexpr int kBoxLanes = 256;
 hipError_t launch_box(int halo, int nfields, bool bf16, const BoxArgs& a, uint32_t nblocks, hipStream_t st);
 hipError_t launch_finalize(const double* partials, int nparts, double inv_m, float* loss, hipStream_t st);
 hipError_t launch_scale(void* grad, bool bf16, int64_t n, const float* grad_out, hipStream_t st);

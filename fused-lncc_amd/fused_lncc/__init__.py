@@ -110,7 +110,7 @@ class _FusedLNCC(torch.autograd.Function):
         else:
             # the library reads (N, C, D, H, W) as N*C volumes; grad comes back in pred's shape
             pf, tf = pred, target
-            if need and need_t:  # one pass for both gradients
+            if need and need_t:  # both gradients: the pred pass, then the swapped one
                 loss, grad, gt = ext.loss_grad_pt(pf, tf, kernel_size, smooth_dr)
             else:
                 loss, grad = ext.loss_grad(pf, tf, kernel_size, smooth_dr, need)

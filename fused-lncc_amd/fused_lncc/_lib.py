@@ -38,6 +38,7 @@ SIGNATURES = {
     "fl_lncc_maps": (_I, [_P, _P, _I, _L, _L, _L, _L, _I, _F, _P, _P, _P, _P, _P]),
     "fl_lncc_backward": (_I, [_P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _I, _F, _P, _P]),
     "fl_box3d": (_I, [_P, _P, _L, _L, _L, _L, _I, _P]),
+    "fl_test_set_dchunk": (_I, [_I]),
 }
 
 _lib = None
@@ -66,6 +67,22 @@ def load():
             fn.argtypes = args
         _lib = lib
     return _lib
+
+
+class dchunk:
+    """Test hook: launches on this thread inside the block split D into chunks of `planes` output
+    planes (clamped to D); the launch planner decides again on exit."""
+
+    def __init__(self, planes):
+        self.planes = int(planes)
+
+    def __enter__(self):
+        check(load().fl_test_set_dchunk(self.planes))
+        return self
+
+    def __exit__(self, *exc):
+        load().fl_test_set_dchunk(0)
+        return False
 
 
 def check(rc):

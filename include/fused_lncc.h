@@ -89,9 +89,9 @@ int fl_lncc_finalize(const void* workspace, int64_t B, int64_t D, int64_t H, int
  * d loss / d target (each in the input dtype, already multiplied by -1/M), all required. No
  * counterpart in the reference, whose gradient goes to pred only (its README.md:116-121); it is
  * the target-side gradient that FireANTs computes for symmetric registration. The loss is symmetric
- * in its two inputs, so the target gradient is the pred gradient with the two swapped: for k <= 7
- * one fused kernel carries both (five adjoint fields instead of three), for k = 9 it runs as two
- * passes of the pred-gradient kernel. Same workspace as fl_lncc_loss_grad.
+ * in its two inputs, so the target gradient is the pred gradient with the two swapped: two passes
+ * of the pred-gradient kernel (the second one's partial sums are not reduced). Same workspace as
+ * fl_lncc_loss_grad.
  */
 int fl_lncc_loss_grad_pt(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,
                          int64_t W, int kernel_size, float smooth_dr, float* loss, void* grad_pred,
@@ -124,6 +124,15 @@ int fl_lncc_backward(const float* A, const float* Bc, const float* Cc, const voi
 
 /* y = zero-padded k^3 box-sum of x, float32 — box3d_sep_forward, fused_lncc/csrc/lncc3d.cu:329-344. */
 int fl_box3d(const float* x, float* y, int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size, void* stream);
+
+/*
+ * Test hook, no counterpart in the reference: makes every launch planned afterwards on the calling
+ * thread split D into chunks of `planes` output planes (clamped to D; 0 restores the launch
+ * planner, which picks the split for the device's compute-unit count). Tests use it to put chunk
+ * seams into small volumes and to march long volumes unsplit. Thread-local: other threads keep
+ * the planner. Returns FL_OK, or FL_E_SHAPE for a negative length.
+ */
+int fl_test_set_dchunk(int planes);
 
 #ifdef __cplusplus
 }

@@ -179,3 +179,138 @@ float lncc_oracle_round_bf16(float x) {
     memcpy(&y, &u, 4);
     return y;
 }
+
+/*
+ * The reference kernel's own float32 arithmetic, restated (fused_lncc/csrc/lncc3d.cu): the
+ * error level the GPU path is measured against on ill-conditioned inputs (offset intensities,
+ * zero and constant regions). Not a second oracle: the float64 functions above are the exact
+ * values; this gives what the reference itself returns for the same float32 inputs.
+ *   - box-sums as direct k-tap sums in float32, x then y then z, each tap added in order with
+ *     the products fused (the CUDA compiler contracts `app += p * p` to an fma):
+ *     lncc3d.cu:57-92 (forward), lncc3d.cu:195-227 (backward);
+ *   - cross, clamped variances, ncc and the adjoints with IEEE divisions: lncc3d.cu:93-107;
+ *   - grad = scale * (box A + 2 p box B + t box C) with scale 1 (lncc3d.cu:231-233), then the
+ *     float32 tensor multiply by -1/M of fused_lncc/__init__.py:73.
+ * The loss is 1 - mean(ncc) with the mean taken in float64 (torch's float32 mean differs from it
+ * by far less than the errors this is used to bound).
+ */
+static void ref32_axis(const float* in, float* out, int len, long stride, int h, long outer,
+                       long ostride, long inner, long istride) {
+    for (long o = 0; o < outer; ++o)
+        for (long i = 0; i < inner; ++i) {
+            const float* src = in + o * ostride + i * istride;
+            float* dst = out + o * ostride + i * istride;
+            for (int x = 0; x < len; ++x) {
+                float s = 0.f;
+                for (int d = -h; d <= h; ++d) {
+                    int j = x + d;
+                    s += (j >= 0 && j < len) ? src[(long)j * stride] : 0.f;
+                }
+                dst[(long)x * stride] = s;
+            }
+        }
+}
+
+/* One float32 field box-summed in the reference's order; `x` already holds the x-tap input. */
+static void ref32_box(const float* x, float* y, float* tmp, int D, int H, int W, int h) {
+    long HW = (long)H * W;
+    ref32_axis(x, tmp, W, 1, h, (long)D * H, W, 1, 1);
+    ref32_axis(tmp, y, H, W, h, D, HW, W, 1);
+    ref32_axis(y, tmp, D, HW, h, 1, 0, HW, 1);
+    memcpy(y, tmp, sizeof(float) * D * HW);
+}
+
+/* x-pass of a product field: s = fma(a_j, b_j, s) over the taps (lncc3d.cu:62-67). */
+static void ref32_xprod(const float* a, const float* b, float* out, int D, int H, int W, int h) {
+    for (long r = 0; r < (long)D * H; ++r)
+        for (int x = 0; x < W; ++x) {
+            float s = 0.f;
+            for (int d = -h; d <= h; ++d) {
+                int j = x + d;
+                float u = (j >= 0 && j < W) ? a[r * W + j] : 0.f;
+                float v = (j >= 0 && j < W) ? b[r * W + j] : 0.f;
+                s = fmaf(u, v, s);
+            }
+            out[r * W + x] = s;
+        }
+}
+
+static int ref32_volume(const float* p, const float* t, int D, int H, int W, int k, float dr,
+                        double M, float* g, float* ncc_map, double* ncc_sum) {
+    long V = (long)D * H * W, HW = (long)H * W;
+    int h = k / 2;
+    float n = (float)(k * k * k);
+    float* buf = (float*)malloc(sizeof(float) * V * 10);
+    if (!buf) return 1;
+    float *Sp = buf, *St = buf + V, *Spp = buf + 2 * V, *Stt = buf + 3 * V, *Spt = buf + 4 * V;
+    float *A = buf + 5 * V, *Bm = buf + 6 * V, *Cm = buf + 7 * V, *tmp = buf + 8 * V, *x = buf + 9 * V;
+    /* x-pass of the five fields, then y and z (the reference stages x-sums, y-sums, z-sums) */
+    ref32_axis(p, x, W, 1, h, (long)D * H, W, 1, 1);
+    ref32_axis(x, tmp, H, W, h, D, HW, W, 1);
+    ref32_axis(tmp, Sp, D, HW, h, 1, 0, HW, 1);
+    ref32_axis(t, x, W, 1, h, (long)D * H, W, 1, 1);
+    ref32_axis(x, tmp, H, W, h, D, HW, W, 1);
+    ref32_axis(tmp, St, D, HW, h, 1, 0, HW, 1);
+    float* outs[3] = {Spp, Stt, Spt};
+    const float* fa[3] = {p, t, p};
+    const float* fb[3] = {p, t, t};
+    for (int f = 0; f < 3; ++f) {
+        ref32_xprod(fa[f], fb[f], x, D, H, W, h);
+        ref32_axis(x, tmp, H, W, h, D, HW, W, 1);
+        ref32_axis(tmp, outs[f], D, HW, h, 1, 0, HW, 1);
+    }
+    double acc = 0.0;
+    for (long i = 0; i < V; ++i) {
+        float cross = Spt[i] - Sp[i] * St[i] / n;
+        float vp = fmaxf(Spp[i] - Sp[i] * Sp[i] / n, 0.f) + dr;
+        float vt = fmaxf(Stt[i] - St[i] * St[i] / n, 0.f) + dr;
+        float ncc = (cross * cross) / (vp * vt);
+        float a = 0.f, b = 0.f, c = 0.f;
+        if (ncc < 1.0f) {
+            c = 2.f * cross / (vp * vt);
+            b = -(cross * cross) / (vp * vp * vt);
+            a = -fmaf(St[i], c, 2.f * Sp[i] * b) / n;
+        } else if (ncc >= 1.0f) {
+            ncc = 1.0f;
+        }
+        acc += ncc;
+        if (ncc_map) ncc_map[i] = ncc;
+        A[i] = a;
+        Bm[i] = b;
+        Cm[i] = c;
+    }
+    *ncc_sum = acc;
+    if (g) {
+        float* bA = Sp; /* the box-sums are no longer needed */
+        float* bB = St;
+        float* bC = Spp;
+        ref32_box(A, bA, tmp, D, H, W, h);
+        ref32_box(Bm, bB, tmp, D, H, W, h);
+        ref32_box(Cm, bC, tmp, D, H, W, h);
+        float sc = (float)(-1.0 / M);
+        for (long i = 0; i < V; ++i) g[i] = fmaf(t[i], bC[i], fmaf(2.f * p[i], bB[i], bA[i])) * sc;
+    }
+    free(buf);
+    return 0;
+}
+
+/* Loss, optional gradient wrt pred (float32, times -1/M) and optional ncc map (float32) as the
+ * reference kernel computes them in float32. Returns 0, or -1 on allocation failure. */
+int lncc_oracle_ref32(const float* pred, const float* target, int B, int D, int H, int W, int k,
+                      float dr, double* loss_out, float* grad, float* ncc_map) {
+    long V = (long)D * H * W;
+    double M = (double)B * V;
+    double total = 0.0;
+    int err = 0;
+#pragma omp parallel for schedule(dynamic) reduction(+ : total) reduction(| : err)
+    for (int b = 0; b < B; ++b) {
+        long o = (long)b * V;
+        double s = 0.0;
+        err |= ref32_volume(pred + o, target + o, D, H, W, k, dr, M, grad ? grad + o : NULL,
+                            ncc_map ? ncc_map + o : NULL, &s);
+        total += s;
+    }
+    if (err) return -1;
+    *loss_out = 1.0 - total / M;
+    return 0;
+}

@@ -35,6 +35,8 @@ def lib():
         L.lncc_oracle.restype = ctypes.c_int
         L.lncc_oracle_box3d.argtypes = [dp, dp] + [ctypes.c_int] * 5
         L.lncc_oracle_box3d.restype = None
+        L.lncc_oracle_ref32.argtypes = [fp, fp] + [ctypes.c_int] * 5 + [ctypes.c_float, dp, fp, fp]
+        L.lncc_oracle_ref32.restype = ctypes.c_int
         L.lncc_oracle_round_bf16.argtypes = [ctypes.c_float]
         L.lncc_oracle_round_bf16.restype = ctypes.c_float
         _lib = L
@@ -72,6 +74,28 @@ def lncc(pred, target, k, smooth_dr=1e-5, policy=POLICY_KERNEL, grad=True, maps=
         raise MemoryError("oracle allocation failed")
     if maps:
         return loss.value, g, dict(zip(("ncc", "A", "B", "C"), mp))
+    return loss.value, g
+
+
+def lncc_ref32(pred, target, k, smooth_dr=1e-5, grad=True, ncc_map=False):
+    """What the reference kernel itself returns in float32 for these inputs (its direct k-tap
+    float32 box-sums and IEEE divisions, fused_lncc/csrc/lncc3d.cu): loss (float), gradient wrt pred
+    (float32 array or None) and, with ncc_map=True, the float32 ncc map. Used to bound the GPU
+    path's error on ill-conditioned inputs by the reference's own error against the float64
+    oracle."""
+    p, t = _f32(pred), _f32(target)
+    assert p.shape == t.shape
+    B, D, H, W = _bdhw(p.shape)
+    loss = ctypes.c_double(0.0)
+    g = np.empty(p.shape, np.float32) if grad else None
+    m = np.empty(p.shape, np.float32) if ncc_map else None
+    rc = lib().lncc_oracle_ref32(_ptr(p, ctypes.c_float), _ptr(t, ctypes.c_float), B, D, H, W, int(k),
+                                 float(smooth_dr), ctypes.byref(loss), _ptr(g, ctypes.c_float),
+                                 _ptr(m, ctypes.c_float))
+    if rc != 0:
+        raise MemoryError("oracle allocation failed")
+    if ncc_map:
+        return loss.value, g, m
     return loss.value, g
 
 

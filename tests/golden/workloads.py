@@ -82,6 +82,38 @@ def randn_pair(shape, seed, dtype=torch.float32):
     return p.to(dtype).contiguous(), t.to(dtype).contiguous()
 
 
+def structured_pair(shape, kind, seed, axis=None, start=0, fill=0.0):
+    """Pred/target pairs with the structure real volumes have, float32 on the CPU:
+
+    * ``unit``   target ~ U[0,1), pred = 0.7*target + 0.3*U[0,1) (intensities scaled to [0,1]);
+    * ``byte``   integer intensities: target ~ U{0..255}, pred = clip(target + U{-24..24}, 0, 255);
+    * ``offset`` target = 100 + N(0,1), pred = 100 + 0.8*(target - 100) + 0.6*N(0,1): unit
+      contrast on a large offset, where the variances cancel most digits of the box-sums.
+
+    With ``axis`` (2 = D, 3 = H, 4 = W of the (N,C,D,H,W) shape) both volumes are set to ``fill``
+    from index ``start`` on along that axis: an exactly zero background, or a constant one, after
+    the signal, as in skull-stripped or padded scans."""
+    g = _gen(seed)
+    if kind == "unit":
+        t = torch.rand(shape, generator=g)
+        p = 0.7 * t + 0.3 * torch.rand(shape, generator=g)
+    elif kind == "byte":
+        t = torch.randint(0, 256, shape, generator=g).float()
+        p = (t + torch.randint(-24, 25, shape, generator=g).float()).clamp(0, 255)
+    elif kind == "offset":
+        n = torch.randn(shape, generator=g)
+        t = 100.0 + n
+        p = 100.0 + 0.8 * n + 0.6 * torch.randn(shape, generator=g)
+    else:
+        raise KeyError(kind)
+    if axis is not None:
+        idx = [slice(None)] * len(shape)
+        idx[axis] = slice(start, None)
+        t[tuple(idx)] = fill
+        p[tuple(idx)] = fill
+    return p.contiguous(), t.contiguous()
+
+
 def checksum(x):
     """Order-fixed float64 digest of a tensor: (sum, sum of squares, weighted sum)."""
     a = x.detach().to(torch.float64).reshape(-1).cpu().numpy()

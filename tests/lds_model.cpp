@@ -1,6 +1,5 @@
 // Host-side model of the LDS accesses of the fused LNCC kernel (lncc_fused_kernel.h): for every
-// halo h = 1..4, both adjoint-field counts (3; 5 where the kernel has that mode, h <= 3) and both
-// row-read lengths of the AX units, it enumerates the LDS reads and writes of every lane in every
+// halo h = 1..4 (tile 32 x 32, and 32 x 24 at h = 4) it enumerates the LDS reads and writes of every lane in every
 // stage from the same lane maps the kernel uses (lncc_geometry.h) and checks
 //   bounds    every access lies inside its __shared__ array (spare floats included);
 //   races     within a phase no address is written twice, and no array written in a phase is read
@@ -67,13 +66,13 @@ struct Model {
     }
 };
 
-template <int H, int NA>
-long check(int plant, bool early_unit_rows) {
-    using G = fl::Geo<H, NA>;
+template <int H>
+long check(int plant) {
+    using G = fl::Geo<H>;
+    constexpr int NA = G::NADJ;
     Model m;
     m.plant = plant;
-    m.cfg = "h=" + std::to_string(H) + " fields=" + std::to_string(NA) +
-            (early_unit_rows ? " unit rows of SX+2h" : " unit rows of S+2h");
+    m.cfg = "h=" + std::to_string(H) + " tile 32x" + std::to_string(G::TY);
     m.size = {5L * G::ZP + G::PAD, 5L * G::XP + G::PAD, (long)NA * G::GP + G::PAD,
               (long)NA * G::GXP + G::PAD, (long)NA * G::GYP};
     for (int p = 0; p < 2; ++p) {
@@ -81,7 +80,7 @@ long check(int plant, bool early_unit_rows) {
         for (int a = 0; a < NARR; ++a) m.writes[p][a].assign(m.size[a], 0);
     }
     const int rows_x = fl::rup4(G::SX + 2 * H);                       // X row read (floats)
-    const int rows_a = fl::rup4((early_unit_rows ? G::SX : G::SA) + 2 * H);  // AX row read
+    const int rows_a = fl::rup4(G::SX + 2 * H);  // AX row read: the unit row is read as an X row
     const int rows_y = fl::rup4(G::SY + 2 * H) - (plant == 2 ? 1 : 0);
     const int rows_b = fl::rup4(G::SB + 2 * H);
 
@@ -174,7 +173,7 @@ long check(int plant, bool early_unit_rows) {
         // P1 / AZ reads one xy-sum per field of its output column
         if (tid < G::NOUT) {
             int ox, oy;
-            fl::az_lane(tid, ox, oy);
+            fl::az_lane<G>(tid, ox, oy);
             for (int c = 0; c < NA; ++c) {
                 const long a = (long)c * G::GYP + oy * G::GYS + ox;
                 m.read(1, GY, a, 1);
@@ -197,15 +196,10 @@ long check(int plant, bool early_unit_rows) {
 int main(int argc, char** argv) {
     const int plant = argc > 1 ? std::atoi(argv[1]) : 0;
     long f = 0;
-    for (bool early : {false, true}) {
-        f += check<1, 3>(plant, early);
-        f += check<2, 3>(plant, early);
-        f += check<3, 3>(plant, early);
-        f += check<4, 3>(plant, early);
-        f += check<1, 5>(plant, early);
-        f += check<2, 5>(plant, early);
-        f += check<3, 5>(plant, early);
-    }
+    f += check<1>(plant);
+    f += check<2>(plant);
+    f += check<3>(plant);
+    f += check<4>(plant);
     std::printf("%s\n", f ? "FAILED" : "all ok");
     return f ? 1 : 0;
 }

@@ -1,0 +1,179 @@
+"""Numerics of the HIP path on the inputs where float32 box-sums are ill-conditioned, against the
+float64 oracle, with the reference's own float32 error (its kernel's arithmetic restated in
+oracle.lncc_ref32) as the yardstick.
+
+* Exactly zero or constant regions after signal (along D over an unsplit march of 144-256 planes,
+  along H and W inside and across tiles), with intensities in [0, 1) and integer intensities in
+  [0, 255]. The reference sums every window directly, so a window that is all zero, or all one
+  representable constant, gives exactly cross = 0, var = 0, ncc = 0 and zero adjoints
+  (fused_lncc/csrc/lncc3d.cu:57-107). Anything else there is not rounding noise: with both
+  variances at the floor dr, any residue r in cross becomes ncc = r^2/dr^2 and adjoints r/dr^2.
+  Where the oracle and the restated reference are both exactly zero (ncc map, gradient), the HIP
+  path must be exactly zero too.
+* Offset intensities (100 + N(0,1)) over a 256-plane march: the variances cancel about four
+  digits of the box-sums.
+* The large workload's first volume from the full (2,16,256^3) launch.
+
+Bounds: the north-star parity bar (loss relative 1e-5, gradient cosine > 0.9999 and relative L2 <
+1e-3), or, where the reference's own error against the float64 oracle is larger, four times that
+error (twice it for the RMS error of the ncc map; for the loss, four times the larger of the
+reference's loss error and the scale of a mean of its per-voxel errors).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import workloads as wl
+from fused_lncc import fused_lncc_loss, lncc_map
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RATIO = 4.0   # the HIP path may be at most this many times further from float64 than the reference
+
+
+def _gpu(p, t, k, dr=1e-5):
+    pd = p.to(DEV).requires_grad_(True)
+    td = t.to(DEV)
+    loss = fused_lncc_loss(pd, td, k, dr)
+    loss.backward()
+    m = lncc_map(pd, td, k, dr)
+    torch.cuda.synchronize()
+    return float(loss.item()), pd.grad.double().cpu().numpy(), m.double().cpu().numpy()
+
+
+def _rel_l2(g, ref):
+    n = np.linalg.norm(ref)
+    return float(np.linalg.norm(g - ref) / n) if n > 0 else float(np.linalg.norm(g))
+
+
+def _cos(g, ref):
+    return float(np.dot(g.ravel(), ref.ravel()) / (np.linalg.norm(g) * np.linalg.norm(ref)))
+
+
+def check_against_oracle(p, t, k, dr=1e-5):
+    """The HIP loss, ncc map and gradient against the float64 oracle, bounded by the parity bar or
+    by RATIO times the error of the reference's own float32 arithmetic."""
+    loss, g, m = _gpu(p, t, k, dr)
+    pn, tn = p.numpy(), t.numpy()
+    l64, g64, maps = O.lncc(pn, tn, k, dr, grad=True, maps=True)
+    m64 = maps["ncc"]
+    l32, g32, m32 = O.lncc_ref32(pn, tn, k, dr, grad=True, ncc_map=True)
+    g64 = g64.astype(np.float64)
+    g32 = g32.astype(np.float64)
+    m32 = m32.astype(np.float64)
+    tag = f"k={k} shape={tuple(p.shape)}"
+
+    # The loss is the mean of the ncc map, so its error is the mean of the per-voxel errors: its
+    # scale is the reference's RMS map error over sqrt(N / k^3) (errors are correlated over a
+    # window), of which the reference's own loss error is one sample.
+    e32 = m32 - m64
+    rms32 = float(np.sqrt(np.mean(e32 * e32)))
+    scale = rms32 * np.sqrt(k ** 3 / e32.size)
+    err_l, err_l32 = abs(loss - l64), abs(l32 - l64)
+    assert err_l <= max(RATIO * max(err_l32, scale), 1e-5 * abs(l64)), \
+        f"{tag}: loss {loss:.9f} oracle {l64:.9f} ref32 {l32:.9f} (error scale {scale:.2e})"
+
+    # exact zeros where the reference's direct sums are exact
+    zm = (m64 == 0) & (m32 == 0)
+    assert np.count_nonzero(m[zm]) == 0, f"{tag}: {np.count_nonzero(m[zm])} of {zm.sum()} exact-zero ncc voxels are not zero (max {np.abs(m[zm]).max():.3e})"
+    zg = (g64 == 0) & (g32 == 0)
+    assert np.count_nonzero(g[zg]) == 0, f"{tag}: {np.count_nonzero(g[zg])} of {zg.sum()} exact-zero gradient voxels are not zero (max {np.abs(g[zg]).max():.3e})"
+
+    err_m, err_m32 = np.abs(m - m64).max(), np.abs(e32).max()
+    assert err_m <= max(RATIO * err_m32, 1e-4), f"{tag}: ncc map max error {err_m:.3e} (reference {err_m32:.3e})"
+    rms = float(np.sqrt(np.mean((m - m64) ** 2)))
+    assert rms <= max(2.0 * rms32, 1e-6), f"{tag}: ncc map RMS error {rms:.3e} (reference {rms32:.3e})"
+
+    if np.linalg.norm(g64) > 0:
+        rel, rel32 = _rel_l2(g, g64), _rel_l2(g32, g64)
+        c = _cos(g, g64)
+        assert rel <= max(RATIO * rel32, 1e-3) and c > 1 - max(RATIO * (1 - _cos(g32, g64)), 1e-4), \
+            f"{tag}: gradient relL2 {rel:.3e} cos {c:.8f} (reference relL2 {rel32:.3e})"
+    return zm.sum(), zg.sum()
+
+
+# ------------------------------------------------------------------ zero / constant regions
+FILL = {("unit", "zero"): 0.0, ("unit", "const"): 0.5, ("byte", "zero"): 0.0, ("byte", "const"): 128.0}
+
+
+@pytest.mark.parametrize("k", [3, 5, 7, 9])
+@pytest.mark.parametrize("fill", ["zero", "const"])
+@pytest.mark.parametrize("kind", ["unit", "byte"])
+def test_slab_after_signal_along_d(kind, fill, k, force_dchunk):
+    """Signal in planes [0, 96), then zero or a constant, over one unsplit 144-plane march."""
+    shape = (1, 2, 144, 40, 48)
+    force_dchunk(shape[2])
+    p, t = wl.structured_pair(shape, kind, 500 + k, axis=2, start=96, fill=FILL[(kind, fill)])
+    nz_m, nz_g = check_against_oracle(p, t, k)
+    assert nz_m > 0 and nz_g > 0   # the case really has exact-zero windows
+
+
+@pytest.mark.parametrize("axis,start", [(3, 20), (4, 44), (4, 11)], ids=["H20", "W44", "W11"])
+@pytest.mark.parametrize("fill", ["zero", "const"])
+@pytest.mark.parametrize("kind", ["unit", "byte"])
+@pytest.mark.parametrize("k", [5, 7])
+def test_slab_after_signal_along_h_w(k, kind, fill, axis, start):
+    """Zero or constant rows/columns after signal: inside the first tile (W11), across a tile
+    boundary (W44, tiles are 32 columns wide) and along H."""
+    shape = (2, 1, 24, 61, 77)
+    p, t = wl.structured_pair(shape, kind, 600 + k + axis, axis=axis, start=start, fill=FILL[(kind, fill)])
+    nz_m, nz_g = check_against_oracle(p, t, k)
+    assert nz_m > 0
+
+
+@pytest.mark.parametrize("k", [5, 7, 9])
+def test_zero_box_in_the_middle(k, force_dchunk):
+    """An exactly zero box in the interior of a volume of [0,255] data: signal before and after it
+    along every axis, one unsplit march."""
+    shape = (1, 1, 130, 70, 70)
+    force_dchunk(shape[2])
+    p, t = wl.structured_pair(shape, "byte", 700 + k)
+    p[..., 40:100, 20:55, 15:60] = 0
+    t[..., 40:100, 20:55, 15:60] = 0
+    nz_m, nz_g = check_against_oracle(p, t, k)
+    assert nz_m > 0 and nz_g > 0
+
+
+# ------------------------------------------------------------------ cancellation, long marches
+@pytest.mark.parametrize("k", [3, 5, 7, 9])
+def test_offset_intensities_long_march(k, force_dchunk):
+    """100 + N(0,1) over one unsplit 256-plane march: bounded by the reference's own float32
+    error on the same input."""
+    shape = (1, 2, 256, 32, 40)
+    force_dchunk(shape[2])
+    p, t = wl.structured_pair(shape, "offset", 800 + k)
+    check_against_oracle(p, t, k)
+
+
+@pytest.mark.parametrize("kind", ["unit", "byte"])
+def test_long_march_unsplit(kind, force_dchunk):
+    """Well-conditioned data over one unsplit 320-plane march at k = 7."""
+    shape = (1, 1, 320, 36, 44)
+    force_dchunk(shape[2])
+    p, t = wl.structured_pair(shape, kind, 900)
+    check_against_oracle(p, t, 7)
+
+
+def test_large_workload_first_volume():
+    """The large workload (2,16,256^3) fp32 k=7 in one launch; its first volume's ncc sum and
+    gradient (scaled by the ratio of the voxel counts) against the float64 oracle of that volume
+    alone (every (N,C) volume is independent). The launch marches 256 planes per workgroup."""
+    p, t = wl.make_inputs("large")
+    pd = p.to(DEV).requires_grad_(True)
+    td = t.to(DEV)
+    loss = fused_lncc_loss(pd, td, 7)
+    loss.backward()
+    m = lncc_map(pd, td, 7)
+    torch.cuda.synchronize()
+    nsum = float(m[0, 0].double().sum().item())
+    g0 = pd.grad[0, 0].double().cpu().numpy() * (p.numel() / p[0, 0].numel())
+    del pd, td, m
+    p0, t0 = p[0, 0:1].unsqueeze(0).numpy(), t[0, 0:1].unsqueeze(0).numpy()
+    del p, t
+    l64, gr = O.lncc(p0, t0, 7)
+    nsum64 = (1.0 - l64) * p0.size
+    assert abs(nsum - nsum64) <= 1e-5 * abs(nsum64), (nsum, nsum64)
+    gr = gr.reshape(g0.shape).astype(np.float64)
+    assert _cos(g0, gr) > 0.9999 and _rel_l2(g0, gr) < 1e-3, (_cos(g0, gr), _rel_l2(g0, gr))
+    assert 0.0 < loss.item() < 1.0

@@ -206,11 +206,11 @@ def test_nonfinite_input_gives_nonfinite_loss(bad):
 
 
 def test_plan_follows_device_cus():
-    """The D-chunk plan is made for the device's compute units: the MRI-shaped volume (42 tiles of
-    32 x 32 per plane) is split into as many chunks as fill the CUs in one round."""
+    """The D-chunk plan is made for the device's compute units: the MRI-shaped volume (56 tiles of
+    32 x 24 per plane at k = 9) is split into as many chunks as fill the CUs in one round."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     nblocks = ext.workspace_bytes((1, 160, 192, 224), 9) // 8
-    assert nblocks % 42 == 0 and nblocks <= cus < nblocks + 42, (nblocks, cus)
+    assert nblocks % 56 == 0 and nblocks <= cus < nblocks + 56, (nblocks, cus)
 
 
 def test_many_volumes():
@@ -224,10 +224,10 @@ def test_many_volumes():
 
 @pytest.mark.parametrize("k", [3, 7, 9])
 @pytest.mark.parametrize("dchunk", [1, 3, 8])
-def test_d_chunk_seams(k, dchunk, monkeypatch):
-    """Workgroups that own short D chunks restart the running z-sums at every chunk: forcing the
-    chunk length (FUSED_LNCC_DCHUNK, read at each launch) puts many seams into one volume."""
-    monkeypatch.setenv("FUSED_LNCC_DCHUNK", str(dchunk))
+def test_d_chunk_seams(k, dchunk, force_dchunk):
+    """Workgroups that own short D chunks restart their z-sums at every chunk: forcing the chunk
+    length (the library's test hook) puts many seams into one volume."""
+    force_dchunk(dchunk)
     p, t = wl.randn_pair((1, 2, 37, 30, 41), 40 + k)
     loss, g, _ = fused(p, t, k)
     lr, gr = O.lncc(p.numpy(), t.numpy(), k)

@@ -1,7 +1,8 @@
 """Randomized parity sweep: many small shapes (edges smaller than the halo, one-plane volumes,
 ragged tiles), every kernel size, both dtypes, against the CPU oracle with the parity bar.
-The second sweep asks for both gradients (target_grad=True: the one-pass kernel for k <= 7, two
-passes for k = 9) and forces short D-chunks on some cases, so chunk seams land inside the volume.
+The second sweep asks for both gradients (target_grad=True: the pred-gradient kernel, then the
+same kernel with the inputs swapped) and forces short D-chunks on some cases, so chunk seams land
+inside the volume.
 Seeded, so every run draws the same cases; each case prints its parameters on failure."""
 import random
 
@@ -76,10 +77,10 @@ def _cases_both(n=40, seed=23):
 
 @pytest.mark.parametrize("case", _cases_both(),
                          ids=lambda c: f"{c[0]}-k{c[1]}-{'x'.join(map(str, c[2]))}-{c[3]}-dc{c[5]}")
-def test_random_shapes_both_gradients(case, monkeypatch):
+def test_random_shapes_both_gradients(case, force_dchunk):
     i, k, shape, dt, corr, dchunk = case
     if dchunk:
-        monkeypatch.setenv("FUSED_LNCC_DCHUNK", str(dchunk))
+        force_dchunk(dchunk)
     p, t = wl.randn_pair(shape, 900 + i)
     if corr:
         p = 0.85 * t + 0.15 * p

@@ -86,14 +86,14 @@ def test_target_grad_compiled_matches_eager():
 @pytest.mark.parametrize("k", [3, 5, 7, 9])
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("dchunk", [None, 3])
-def test_dual_kernel_against_single_passes(k, dt, dchunk, monkeypatch):
-    """The one-pass kernel for both gradients (k <= 7; two passes at k = 9) gives the pred
-    gradient of the pred-only kernel bit for bit (same sums in the same order) and the target
-    gradient of that kernel run with the inputs swapped, on a ragged shape with D-chunk seams."""
+def test_dual_kernel_against_single_passes(k, dt, dchunk, force_dchunk):
+    """The entry point for both gradients gives the pred gradient of the pred-only kernel bit for
+    bit and the target gradient of that kernel run with the inputs swapped, on a ragged shape with
+    D-chunk seams."""
     from fused_lncc import ext
 
     if dchunk is not None:
-        monkeypatch.setenv("FUSED_LNCC_DCHUNK", str(dchunk))
+        force_dchunk(dchunk)
     p, t = wl.randn_pair((2, 1, 19, 37, 45), 120 + k)
     pf = p.reshape(2, 19, 37, 45).to(dt).to(DEV)
     tf = t.reshape(2, 19, 37, 45).to(dt).to(DEV)

@@ -71,8 +71,8 @@ def test_errors_before_device_work():
     # the adjoint maps are all given or all omitted
     rc = lib.fl_lncc_maps(8, 8, 0, 1, 8, 8, 8, 7, 1e-5, 8, 8, None, 8, None)
     assert rc == _lib.FL_E_NULL and "all NULL" in lib.fl_last_error().decode()
-    # both gradients: every pointer is required, the workspace is checked on the one-pass path
-    # (k <= 7) and on the two-pass path (k = 9), and the shape before either
+    # both gradients: every pointer is required, the workspace is checked for every k, and the
+    # shape before either
     for k in (3, 7, 9):
         rc = lib.fl_lncc_loss_grad_pt(8, 8, 0, 1, 8, 8, 8, k, 1e-5, 8, 8, None, 8, 64, None)
         assert rc == _lib.FL_E_NULL and "NULL" in lib.fl_last_error().decode()
@@ -98,7 +98,8 @@ def test_workspace_bytes():
 def test_lds_bytes():
     lib = _lib.load()
     sizes = [lib.fl_lds_bytes(k, _lib.FL_F32) for k in (3, 5, 7, 9)]
-    assert all(0 < b <= 160 * 1024 for b in sizes) and sizes == sorted(sizes)
+    # k = 9 runs on a 32 x 24 tile, so it needs less than k = 7 on 32 x 32
+    assert all(0 < b <= 160 * 1024 for b in sizes) and sizes[:3] == sorted(sizes[:3])
     assert lib.fl_lds_bytes(7, _lib.FL_BF16) == sizes[2]
     assert lib.fl_lds_bytes(8, _lib.FL_F32) == 0 and lib.fl_lds_bytes(7, 5) == 0
 
@@ -115,6 +116,24 @@ def test_shape_limits_without_overflow():
     # host (nothing is launched)
     assert lib.fl_box3d(8, 8, 2 ** 26, 1, 128, 128, 7, None) == _lib.FL_E_SHAPE
     assert "too many" in lib.fl_last_error().decode()
+
+
+def test_grid_in_lanes_fits_32_bits():
+    """A launch's grid counted in lanes must fit in 32 bits: 1024 lanes per workgroup of the fused
+    kernel (one workgroup per 32 x 32 tile and volume at least), 256 per box-kernel workgroup (one
+    per 16 x 16 tile). The boundary is exact on both sides, and the error comes from the host."""
+    lib = _lib.load()
+    # 1024 x 1024 planes: 32 x 32 = 1024 fused tiles per volume; 4096 volumes = 2^22 tiles = 2^32 lanes
+    assert lib.fl_validate(_lib.FL_F32, 7, 4095, 1, 1024, 1024) == _lib.FL_OK
+    assert lib.fl_validate(_lib.FL_F32, 7, 4096, 1, 1024, 1024) == _lib.FL_E_SHAPE
+    assert "too many" in lib.fl_last_error().decode()
+    assert lib.fl_workspace_bytes(4096, 1, 1024, 1024, 7) == 0
+    rc = lib.fl_lncc_loss_grad(8, 8, _lib.FL_F32, 4096, 1, 1024, 1024, 7, 1e-5, 8, 8, 8, 1 << 40, None)
+    assert rc == _lib.FL_E_SHAPE
+    # box kernel: 64 x 64 = 4096 tiles of 16 x 16 per 1024^2 plane; 2^12 volumes = 2^24 tiles = 2^32 lanes
+    assert lib.fl_box3d(8, 8, 4096, 1, 1024, 1024, 7, None) == _lib.FL_E_SHAPE
+    assert "too many" in lib.fl_last_error().decode()
+    assert lib.fl_lncc_backward(8, 8, 8, 8, 8, _lib.FL_F32, 4096, 1, 1024, 1024, 7, 1.0, 8, None) == _lib.FL_E_SHAPE
 
 
 def test_python_api_errors():
