@@ -49,12 +49,17 @@
 namespace fl {
 
 // Loads NV consecutive floats from a 16-byte aligned LDS address as float4s (the last one may
-// read up to 3 floats past the row; they are not used).
+// read up to 3 floats past the row; they are not used). Each float4 passes through an empty asm
+// operand that needs all four lanes, so that the loads stay 128-bit reads: otherwise the
+// optimizer re-partitions them along the box-sums' blocks (a row of 10 floats became b128 + b96 +
+// read2_b32 + b32 instead of b128 + b128 + b64), which costs LDS instructions and bank cycles.
+typedef float lds_f4 __attribute__((ext_vector_type(4)));
 template <int NV>
 __device__ __forceinline__ void lds_row(const float* __restrict__ src, float (&v)[NV]) {
 #pragma unroll
     for (int m = 0; m < (NV + 3) / 4; ++m) {
-        const float4 f = reinterpret_cast<const float4*>(src)[m];
+        lds_f4 f = reinterpret_cast<const lds_f4*>(src)[m];
+        asm("" : "+v"(f));
         v[4 * m] = f.x;
         if (4 * m + 1 < NV) v[4 * m + 1] = f.y;
         if (4 * m + 2 < NV) v[4 * m + 2] = f.z;
