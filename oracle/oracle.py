@@ -108,6 +108,21 @@ def box3d(x, k):
     return y
 
 
+def round_bf16_np(x):
+    """round_bf16 for whole arrays (finite values): float32 -> bfloat16 bits by round to nearest,
+    ties to even, back to float32."""
+    u = _f32(x).view(np.uint32)
+    u = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    return u.view(np.float32)
+
+
+def bf16_ulp(x):
+    """The spacing of bfloat16 numbers (8 significant bits) at |x|, elementwise, float64."""
+    a = np.abs(np.asarray(x, np.float64))
+    _, e = np.frexp(a)
+    return np.where(a > 0, np.ldexp(1.0, e - 8), 0.0)
+
+
 def round_bf16(x):
     """float32 -> bfloat16 (round to nearest even) -> float32, elementwise, via the C routine."""
     f = lib().lncc_oracle_round_bf16

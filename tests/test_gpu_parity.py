@@ -55,6 +55,23 @@ def assert_grad(g, gr, cos_min=GRAD_COS, rel_max=GRAD_REL_L2):
     assert c > cos_min and r < rel_max, f"cos={c:.8f} relL2={r:.3e}"
 
 
+def assert_grad_bf16(g, gr):
+    """A bfloat16 gradient against the float32 oracle gradient of the same (bf16-representable)
+    inputs: the kernel accumulates in float32 and rounds once to nearest even, so the gradient is
+    the oracle's rounded to bf16 up to the float32 error: within one bf16 ulp of round_bf16(oracle)
+    everywhere (plus 1e-5 of the gradient's scale for elements near zero), relative L2 error <=
+    3e-3 (one rounding to 8 significant bits costs ~1.1e-3) and cosine > 0.9999. The reference's
+    own bf16 checks are looser (tests/test_bf16.py:10-21)."""
+    g = np.asarray(g, np.float64).ravel()
+    gr = np.asarray(gr, np.float64).ravel()
+    c, r = cos_rel(g, gr)
+    assert c > 0.9999 and r <= 3e-3, f"bf16 gradient cos={c:.8f} relL2={r:.3e}"
+    rb = O.round_bf16_np(gr).astype(np.float64)
+    tol = O.bf16_ulp(rb) + 1e-5 * np.abs(gr).max()
+    bad = np.abs(g - rb) > tol
+    assert not bad.any(), f"{bad.sum()} of {bad.size} bf16 gradient elements more than one ulp from the rounded oracle"
+
+
 def assert_loss(l, lr, rtol):
     assert abs(l - lr) <= rtol * abs(lr), f"loss {l:.9f} vs {lr:.9f} (rel {abs(l - lr) / abs(lr):.2e})"
 
@@ -73,7 +90,8 @@ def test_golden_bf16_values():
     loss, g, gdt = fused(d["pred"], d["target"], 7, dtype=torch.bfloat16)
     assert gdt == torch.bfloat16
     assert_loss(loss, float(d["loss"]), LOSS_RTOL_BF16)
-    assert_grad(g, d["grad"], 0.999, 1e-2)
+    assert_grad(g, d["grad"], 0.999, 1e-2)   # the reference's own bar
+    assert_grad_bf16(g, d["grad"])
 
 
 # ---------------------------------------------------------------- reference tests, restated
@@ -110,7 +128,8 @@ def test_bf16_matches_fp32_of_same_values(k):
     lf, gf, _ = fused(p.float(), t.float(), k)
     assert abs(lb - lf) < 1e-3
     assert_loss(lb, lf, LOSS_RTOL_BF16)
-    assert np.abs(gb - gf).mean() / np.abs(gf).mean() < 2e-2
+    assert np.abs(gb - gf).mean() / np.abs(gf).mean() < 2e-2   # the reference's own bar
+    assert_grad_bf16(gb, gf)
 
 
 @pytest.mark.parametrize("k", [3, 5, 7, 9])
@@ -352,8 +371,10 @@ def test_maximum_plane_size(dtype):
     loss_s, g_s = ext.loss_grad(ps.to(DEV), ts.to(DEV), k, 1e-5)
     lr, gr = O.lncc(ps.float().numpy(), ts.float().numpy(), k)
     assert abs(loss_s.item() - lr) <= (1e-5 if dtype == torch.float32 else 1e-2) * abs(lr)
-    assert_grad(gr, g_s.double().cpu().numpy(), 0.9999 if dtype == torch.float32 else 0.999,
-                1e-3 if dtype == torch.float32 else 2e-2)
+    if dtype == torch.float32:
+        assert_grad(g_s.double().cpu().numpy(), gr)
+    else:
+        assert_grad_bf16(g_s.double().cpu().numpy(), gr)
 
     print(f"max plane: {dtype} ({D}, {H}, {W})", flush=True)
     pb = torch.zeros(1, D, H, W, dtype=dtype, device=DEV)
@@ -369,8 +390,8 @@ def test_maximum_plane_size(dtype):
     rel = float(np.linalg.norm(corner - ref) / np.linalg.norm(ref))
     if dtype == torch.float32:
         assert cos > 0.99999 and rel < 1e-4, (cos, rel)
-    else:  # both gradients are rounded to bf16 once, at different scales
-        assert cos > 0.9999 and rel < 1e-2, (cos, rel)
+    else:  # both gradients are rounded to bf16 once, at different scales: two roundings
+        assert cos > 0.9999 and rel < 4e-3, (cos, rel)
     g_b[0, :, H - ph - m:, W - pw - m:] = 0
     assert g_b.abs().max().item() == 0.0
     # the ncc sum of the plane is the small volume's; the float32 loss 1 - sum/M is within one
@@ -457,7 +478,8 @@ def test_workload_bf16():
     assert gdt == torch.bfloat16
     assert_loss(loss, float(st["loss"]), LOSS_RTOL_BF16)
     lr, gr = O.lncc(p.float().numpy(), t.float().numpy(), 5)
-    assert_grad(g, gr, 0.999, 1e-2)
+    assert_grad(g, gr, 0.999, 1e-2)   # the reference's own bar
+    assert_grad_bf16(g, gr)
 
 
 def test_workload_large_properties():

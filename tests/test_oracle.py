@@ -195,6 +195,56 @@ def test_round_bf16_matches_torch():
     assert np.isnan(O.round_bf16(np.array([np.nan], np.float32))[0])
 
 
+def test_round_bf16_array_form():
+    """The vectorized rounding the bf16 gradient checks use agrees with the C routine and with
+    torch's float32 -> bfloat16 cast on a million values spanning the exponent range, exact ties
+    included; bf16_ulp is the spacing of bfloat16 numbers (2^-7 at 1, halved below each power of
+    two)."""
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(1 << 20, generator=g) * torch.exp(10 * torch.randn(1 << 20, generator=g))).numpy()
+    ties = (np.arange(1, 2001, dtype=np.uint32) << 16 | np.uint32(0x8000)).view(np.float32)
+    x = np.concatenate([x, ties, -ties]).astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(O.round_bf16_np(x), ref)
+    assert np.array_equal(O.round_bf16_np(x[:512]), O.round_bf16(x[:512]))
+    assert O.bf16_ulp(np.array([1.0]))[0] == 2.0 ** -7 and O.bf16_ulp(np.array([0.75]))[0] == 2.0 ** -8
+    # the next bf16 number away from zero is one unit up in the magnitude bits
+    v = ref[:4096][(ref[:4096] != 0) & np.isfinite(ref[:4096])]
+    nxt = (v.view(np.uint32) + np.uint32(1 << 16)).view(np.float32)
+    ok = np.isfinite(nxt)
+    gap = np.abs(nxt[ok].astype(np.float64) - v[ok].astype(np.float64))
+    assert np.array_equal(gap, O.bf16_ulp(v[ok]))
+
+
+@pytest.mark.parametrize("path", FULL, ids=[os.path.basename(p)[:-4] for p in FULL])
+def test_separable_loss_of_the_fixtures(path):
+    """Every fixture also holds the loss of the reference's separable box-sum path
+    (baselines/torch_lncc.py:17-22,40-42, three 1-D convolutions). The float64 oracle matches it at
+    the parity bar, and the restated separable path reproduces it (the degenerate constant fields
+    are rounding noise in the reference: range only)."""
+    import torch_lncc_port as port
+    d = np.load(path)
+    k, dr = int(d["k"]), float(d["smooth_dr"])
+    lsep = float(d["loss_separable"])
+    p, t = torch.from_numpy(d["pred"]), torch.from_numpy(d["target"])
+    ls = float(port.lncc_separable(p, t, k, dr))
+    if os.path.basename(path).startswith("degen_"):
+        assert 0.0 <= lsep <= 1.0 and 0.0 <= ls <= 1.0
+        return
+    lo, _ = O.lncc(d["pred"], d["target"], k, dr, grad=False)
+    assert abs(lo - lsep) <= 1e-5 * abs(lsep), (lo, lsep)
+    assert abs(ls - lsep) <= 1e-6 * abs(lsep), (ls, lsep)
+
+
+def test_separable_box_is_the_dense_box():
+    import torch_lncc_port as port
+    x = torch.randn(2, 3, 9, 11, 13, dtype=torch.float64)
+    for k in (3, 5, 7, 9):
+        a = port.box_separable(x, k)
+        assert torch.allclose(a, port.box_dense(x, k), rtol=1e-12, atol=1e-12)
+        assert np.allclose(a.numpy(), O.box3d(x.numpy(), k), rtol=1e-12, atol=1e-12)
+
+
 @pytest.mark.parametrize("name", ["cpu_k3", "nc_k5", "dr1_k3", "edge_k7_1x3x7x9x11"])
 def test_torch_port_matches_golden(name):
     """The CPU baseline (the reference's naive torch path, restated) reproduces the golden vectors."""
