@@ -157,9 +157,12 @@ class _FusedLNCC(torch.autograd.Function):
             return g, gt, None, None, None, None
         saved = ctx.saved_tensors
         if len(saved) == 4:  # compiled: functional form
+            # multiplied in float32 and rounded once, as the eager scale_grad_ kernel does (a bf16
+            # grad_out would be rounded before the product)
             sg, sgt = saved[2], saved[3]
-            g = (sg * grad_out.to(sg.dtype)).reshape(ctx.shape) if ctx.need else None
-            gt = (sgt * grad_out.to(sgt.dtype)).reshape(ctx.shape) if ctx.need_t else None
+            go = grad_out.float()
+            g = (sg.float() * go).to(sg.dtype).reshape(ctx.shape) if ctx.need else None
+            gt = (sgt.float() * go).to(sgt.dtype).reshape(ctx.shape) if ctx.need_t else None
             return g, gt, None, None, None, None
         pf, tf = saved
         if ctx.need and g is None:

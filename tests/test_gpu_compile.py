@@ -47,6 +47,23 @@ def test_compiled_step_matches_eager(dt, backend):
     assert torch.allclose(gc.float(), ge.float(), rtol=tol, atol=tol * ge.float().abs().max().item())
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_compiled_scaled_loss_matches_eager_bitwise(dt):
+    """grad_out = 3 (the loss weighted in a larger objective): the compiled backward multiplies the
+    stored gradient by grad_out in float32 and rounds once, as the eager in-place scaling kernel
+    does, so the two gradients are equal bit for bit, in bf16 as in fp32."""
+    torch._dynamo.reset()
+    p0, t = _inputs(dt)
+
+    def step(p, t):
+        return 3.0 * fused_lncc_loss(p, t, 7)
+
+    le, ge = _run(step, p0, t)
+    lc, gc = _run(torch.compile(step, backend="aot_eager", fullgraph=True), p0, t)
+    assert gc.dtype == dt
+    assert torch.equal(lc, le) and torch.equal(gc, ge)
+
+
 def test_compiled_step_second_call_and_new_shape():
     torch._dynamo.reset()
     f = torch.compile(_step, backend="aot_eager", fullgraph=True)

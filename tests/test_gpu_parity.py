@@ -135,7 +135,9 @@ def test_bf16_matches_fp32_of_same_values(k):
 @pytest.mark.parametrize("k", [3, 5, 7, 9])
 def test_fused_backward_matches_scatter(k):
     """Reference-API path: maps -> box-sum scatter formula == lncc_backward (tests/test_pytest.py:38-51),
-    and the fused hot-path gradient equals that unfused path."""
+    and the fused hot-path gradient equals that unfused path. The extension is imported by the
+    reference's module name, as its test does."""
+    import fused_lncc_cuda as ext
     p, t = wl.randn_pair((2, 3, 24, 20, 28), 4)
     pf = p.reshape(6, 24, 20, 28).contiguous().to(DEV)
     tf = t.reshape(6, 24, 20, 28).contiguous().to(DEV)

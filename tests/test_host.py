@@ -136,6 +136,14 @@ def test_grid_in_lanes_fits_32_bits():
     assert lib.fl_lncc_backward(8, 8, 8, 8, 8, _lib.FL_F32, 4096, 1, 1024, 1024, 7, 1.0, 8, None) == _lib.FL_E_SHAPE
 
 
+def test_reference_module_name():
+    """`import fused_lncc_cuda` gives the reference's three extension entry points
+    (fused_lncc/csrc/lncc3d.cu:346-350), the same functions as fused_lncc.ext's."""
+    import fused_lncc_cuda
+    for name in ("lncc_forward", "lncc_backward", "box3d_sep_forward"):
+        assert getattr(fused_lncc_cuda, name) is getattr(ext, name)
+
+
 def test_python_api_errors():
     p = torch.randn(1, 1, 8, 8, 8)
     with pytest.raises(AssertionError):
