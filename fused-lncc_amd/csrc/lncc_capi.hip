@@ -155,6 +155,37 @@ int planned(int64_t B, int64_t D, int64_t H, int64_t W, int halo, Plan& p, const
     return FL_OK;
 }
 
+// Scratch of the allocation-free entry point: the per-workgroup ncc partial sums of one launch of
+// the fused kernel, in the library's own device memory. Every call on a device shares that
+// device's copy (calls that overlap on one GPU race); each launch writes the slots it reads, so
+// nothing needs clearing between calls.
+constexpr int64_t kScratchPartials = 65536;  // 512 KiB of float64 per device
+static __device__ __align__(256) double scratch[kScratchPartials];
+
+// The device address of `scratch` on each device, looked up once per device with that device
+// current (each GPU holds its own copy at its own address). Host code uses this address, never the
+// array's name, which on the host is only a stand-in.
+constexpr int kMaxScratchDevices = 64;
+std::atomic<double*> g_scratch_ptr[kMaxScratchDevices];
+
+int scratch_on_current_device(double** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "fl_lncc_loss_grad_noalloc: hipGetDevice");
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return fail(FL_E_DEVICE, "fl_lncc_loss_grad_noalloc: device index " + std::to_string(dev) + " out of range");
+    double* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        void* addr = nullptr;
+        e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || addr == nullptr) return hip_fail(e, "fl_lncc_loss_grad_noalloc: hipGetSymbolAddress(scratch)");
+        p = static_cast<double*>(addr);
+        g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return FL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -250,6 +281,34 @@ int fl_lncc_loss_grad(const void* pred, const void* target, int dtype, int64_t B
                                     workspace_bytes, stream);
     if (rc) return rc;
     return fl_lncc_finalize(workspace, B, D, H, W, kernel_size, loss, stream);
+}
+
+int fl_lncc_loss_grad_noalloc(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,
+                              int64_t W, int kernel_size, float smooth_dr, float* loss, void* grad, void* stream) {
+    int rc = fl_validate(dtype, kernel_size, B, D, H, W);
+    if (rc) return rc;
+    if (!pred || !target || !loss) return fail(FL_E_NULL, "fl_lncc_loss_grad_noalloc: NULL pointer argument");
+    const int halo = kernel_size / 2;
+    Plan p;
+    rc = planned(B, D, H, W, halo, p, "fl_lncc_loss_grad_noalloc");
+    if (rc) return rc;
+    if (p.nblocks > kScratchPartials)
+        return fail(FL_E_WORKSPACE, "fl_lncc_loss_grad_noalloc: the launch needs " + std::to_string(p.nblocks) +
+                                        " partial sums, the library's scratch holds " + std::to_string(kScratchPartials) +
+                                        "; use fl_lncc_loss_grad with a workspace");
+    double* part = nullptr;
+    rc = scratch_on_current_device(&part);
+    if (rc) return rc;
+    fl::FusedArgs a = fused_args(pred, target, B, D, H, W, kernel_size, smooth_dr, p);
+    a.grad = grad;
+    a.partials = part;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = launch_fused(halo, grad ? fl::MODE_GRAD : fl::MODE_LOSS, dtype == FL_BF16, a, (uint32_t)p.nblocks, st);
+    if (e != hipSuccess) return hip_fail(e, "fl_lncc_loss_grad_noalloc: fused kernel launch");
+    const double M = (double)B * (double)D * (double)H * (double)W;
+    e = fl::launch_finalize(part, (int)p.nblocks, 1.0 / M, loss, st);
+    if (e != hipSuccess) return hip_fail(e, "fl_lncc_loss_grad_noalloc: finalize launch");
+    return FL_OK;
 }
 
 int fl_lncc_loss_grad_pt(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,

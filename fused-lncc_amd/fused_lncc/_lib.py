@@ -32,6 +32,7 @@ SIGNATURES = {
     "fl_lds_bytes": (_S, [_I, _I]),
     "fl_lncc_loss_grad": (_I, [_P, _P, _I, _L, _L, _L, _L, _I, _F, _P, _P, _P, _S, _P]),
     "fl_lncc_fused_partials": (_I, [_P, _P, _I, _L, _L, _L, _L, _I, _F, _P, _P, _S, _P]),
+    "fl_lncc_loss_grad_noalloc": (_I, [_P, _P, _I, _L, _L, _L, _L, _I, _F, _P, _P, _P]),
     "fl_lncc_loss_grad_pt": (_I, [_P, _P, _I, _L, _L, _L, _L, _I, _F, _P, _P, _P, _P, _S, _P]),
     "fl_lncc_finalize": (_I, [_P, _L, _L, _L, _L, _I, _P, _P]),
     "fl_scale_grad": (_I, [_P, _I, _L, _P, _P]),

@@ -73,6 +73,20 @@ int fl_lncc_loss_grad(const void* pred, const void* target, int dtype, int64_t B
                       size_t workspace_bytes, void* stream);
 
 /*
+ * fl_lncc_loss_grad without the workspace argument and without any allocation: the per-workgroup
+ * partial sums go to a scratch array in the library's own device memory (512 KiB per GPU, held
+ * until the process ends), so the call makes no hipMalloc/hipFree and no allocating library call.
+ * No counterpart in the reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation). Limit: launches of at most
+ * 65536 workgroups (fl_workspace_bytes(...) <= 512 KiB, e.g. up to 32 volumes of 512^3 at k = 7);
+ * larger ones return FL_E_WORKSPACE. Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (other streams, other threads) race and must be serialized by the caller.
+ * Results are bit-identical to fl_lncc_loss_grad's.
+ */
+int fl_lncc_loss_grad_noalloc(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,
+                              int64_t W, int kernel_size, float smooth_dr, float* loss, void* grad, void* stream);
+
+/*
  * The two launches of fl_lncc_loss_grad, for callers that time or schedule them separately:
  * fl_lncc_fused_partials runs the fused kernel alone (gradient when grad != NULL, one float64 ncc
  * partial sum per workgroup into `workspace`); fl_lncc_finalize reduces those partials in a fixed

@@ -136,6 +136,18 @@ def test_grid_in_lanes_fits_32_bits():
     assert lib.fl_lncc_backward(8, 8, 8, 8, 8, _lib.FL_F32, 4096, 1, 1024, 1024, 7, 1.0, 8, None) == _lib.FL_E_SHAPE
 
 
+def test_no_alloc_entry_point_limits():
+    """The allocation-free entry point refuses, on the host and with a clear message, a launch
+    larger than its static scratch (65536 workgroups), and a missing output pointer."""
+    lib = _lib.load()
+    # 300 volumes of 512 x 512 planes: 300 x 256 tiles of 32 x 32 > 65536 workgroups
+    rc = lib.fl_lncc_loss_grad_noalloc(8, 8, _lib.FL_F32, 300, 4, 512, 512, 7, 1e-5, 8, 8, None)
+    assert rc == _lib.FL_E_WORKSPACE and "scratch holds 65536" in lib.fl_last_error().decode()
+    rc = lib.fl_lncc_loss_grad_noalloc(8, 8, _lib.FL_F32, 1, 4, 8, 8, 7, 1e-5, None, 8, None)
+    assert rc == _lib.FL_E_NULL
+    assert lib.fl_lncc_loss_grad_noalloc(8, 8, _lib.FL_F32, 1, 4, 8, 8, 8, 1e-5, 8, 8, None) == _lib.FL_E_KSIZE
+
+
 def test_reference_module_name():
     """`import fused_lncc_cuda` gives the reference's three extension entry points
     (fused_lncc/csrc/lncc3d.cu:346-350), the same functions as fused_lncc.ext's."""

@@ -1,0 +1,72 @@
+"""fl_lncc_loss_grad_noalloc, the entry point that allocates nothing (its per-workgroup partial
+sums live in the library's static device scratch), against fl_lncc_loss_grad with a caller's
+workspace, through the C ABI: the same kernels in the same order, so loss and gradient must be
+equal bit for bit. Two calls in a row, the second on a smaller input (the scratch keeps the first
+call's contents; nothing may depend on them), for both dtypes, then the first shape again."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import workloads as wl
+from fused_lncc import _lib
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _with_workspace(pf, tf, code, k):
+    lib = _lib.load()
+    B, D, H, W = pf.shape
+    nbytes = lib.fl_workspace_bytes(B, D, H, W, k)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    loss = torch.empty((), dtype=torch.float32, device=DEV)
+    grad = torch.empty_like(pf)
+    _lib.check(lib.fl_lncc_loss_grad(pf.data_ptr(), tf.data_ptr(), code, B, D, H, W, k, 1e-5, loss.data_ptr(),
+                                     grad.data_ptr(), ws.data_ptr(), nbytes, _stream()))
+    return loss, grad
+
+
+def _no_alloc(pf, tf, code, k):
+    lib = _lib.load()
+    B, D, H, W = pf.shape
+    loss = torch.empty((), dtype=torch.float32, device=DEV)
+    grad = torch.empty_like(pf)
+    _lib.check(lib.fl_lncc_loss_grad_noalloc(pf.data_ptr(), tf.data_ptr(), code, B, D, H, W, k, 1e-5,
+                                             loss.data_ptr(), grad.data_ptr(), _stream()))
+    return loss, grad
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_no_alloc_matches_workspace_entry_point(dt):
+    code = _lib.FL_F32 if dt == torch.float32 else _lib.FL_BF16
+    cases = [((6, 40, 48, 56), 7, 11), ((2, 20, 24, 28), 5, 12), ((6, 40, 48, 56), 7, 11)]
+    for shape, k, seed in cases:
+        print(f"no-alloc case {dt} {shape} k={k}", flush=True)
+        p, t = wl.randn_pair(shape, seed)
+        pf, tf = p.to(dt).to(DEV), t.to(dt).to(DEV)
+        l_ws, g_ws = _with_workspace(pf, tf, code, k)
+        l_na, g_na = _no_alloc(pf, tf, code, k)
+        torch.cuda.synchronize()
+        assert torch.equal(l_na, l_ws), (l_na.item(), l_ws.item())
+        assert torch.equal(g_na, g_ws)
+        assert np.isfinite(l_na.item()) and 0.0 < l_na.item() < 1.0
+
+
+def test_no_alloc_loss_only():
+    """grad = NULL: the forward-only kernel, same loss as with a workspace."""
+    lib = _lib.load()
+    p, t = wl.randn_pair((3, 17, 33, 35), 13)
+    pf, tf = p.to(DEV), t.to(DEV)
+    l_ws, _ = _with_workspace(pf, tf, _lib.FL_F32, 3)
+    loss = torch.empty((), dtype=torch.float32, device=DEV)
+    B, D, H, W = pf.shape
+    _lib.check(lib.fl_lncc_loss_grad_noalloc(pf.data_ptr(), tf.data_ptr(), _lib.FL_F32, B, D, H, W, 3, 1e-5,
+                                             loss.data_ptr(), None, _stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(loss, l_ws)
