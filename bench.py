@@ -10,7 +10,9 @@ headline workload (2,16,128,128,128) fp32, k=7 (target ~ N(0,1) seed 0, pred = 0
   launched on, against the 8 TB/s HBM peak; traffic = FETCH_SIZE + WRITE_SIZE per launch from the
   committed rocprofv3 counter summary when present;
 * cpu_baseline: the reference's naive PyTorch LNCC (dense grouped conv3d + autograd, restated in
-  oracle/torch_lncc_port.py) on the host cores, on one of the 32 volumes.
+  oracle/torch_lncc_port.py) on the host cores: one of the 32 volumes of the headline workload
+  (the whole (1,1,32^3) k=3 case with --workload cpu), with the thread count, os.cpu_count() and
+  the CPU model.
 """
 import argparse
 import json
@@ -67,13 +69,21 @@ def _cpu_model():
     return "unknown CPU"
 
 
-def cpu_baseline(k, seconds):
+def cpu_baseline(workload, k, seconds):
+    """The reference's naive PyTorch path (oracle/torch_lncc_port.py) on the host threads torch
+    uses: the whole (1,1,32^3) k=3 case for the cpu workload, otherwise one (N,C) volume of the
+    workload (one 128^3 volume of the headline and bf16 workloads, in fp32; the MRI-shaped volume
+    whole), timed until ``seconds`` of work or 50 runs, median."""
     import torch
 
     import torch_lncc_port
     import workloads as wl
-    shape = (1, 1, 128, 128, 128)
-    p, t = wl.make_inputs("headline", shape)
+    spec = wl.WORKLOADS[workload]
+    shape = spec["shape"] if workload in ("cpu", "mri") else (1, 1, 128, 128, 128)
+    p, t = wl.make_inputs(workload, shape)
+    p, t = p.float(), t.float()
+    for _ in range(2 if workload == "cpu" else 0):   # warm-up of the tiny case
+        torch_lncc_port.loss_and_grad(p, t, k)
     times = []
     t_end = time.perf_counter() + seconds
     while True:
@@ -84,12 +94,18 @@ def cpu_baseline(k, seconds):
             break
     times.sort()
     med = times[len(times) // 2]
-    vox = 128 ** 3
-    return {"value": round(vox * 12 / med / 1e9, 6), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"1 of the 32 volumes, (1,1,128,128,128) fp32 k=7, loss + grad wrt pred; "
-                      f"median of {len(times)} runs = {med * 1e3:.1f} ms "
-                      f"({vox / med / 1e6:.3f} Mvoxel/s) on {torch.get_num_threads()} threads of {_cpu_model()}"}
+    vox = 1
+    for n in shape:
+        vox *= n
+    what = "the whole workload" if workload == "cpu" else (
+        "the volume" if workload == "mri" else f"1 of the {spec['shape'][0] * spec['shape'][1]} volumes")
+    threads = torch.get_num_threads()
+    return {"value": round(vox * 12 / med / 1e9, 6), "unit": "GB/s", "cores": threads,
+            "kind": "port", "ms": round(med * 1e3, 4), "voxels_per_s": round(vox / med, 1),
+            "os_cpu_count": os.cpu_count(), "torch_threads": threads, "cpu_model": _cpu_model(),
+            "sample": f"{what}, {tuple(shape)} fp32 k={k}, loss + grad wrt pred; median of "
+                      f"{len(times)} runs = {med * 1e3:.3f} ms ({vox / med / 1e6:.3f} Mvoxel/s) on "
+                      f"{threads} threads (os.cpu_count() = {os.cpu_count()}) of {_cpu_model()}"}
 
 
 def main():
@@ -195,7 +211,7 @@ def main():
                      "kernel": "lncc_fused_kernel", "algorithmic_bytes_per_launch": alg_bytes},
     }
     if not a.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(k, a.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(a.workload, k, a.cpu_seconds)
     print(json.dumps(out), flush=True)
 
 

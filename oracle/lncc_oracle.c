@@ -22,7 +22,9 @@
  * Pinning (tests/test_oracle.py): golden vectors written from baselines/torch_lncc.py (loss and
  * autograd gradient), brute-force box-sums on tiny volumes, the constant-field closed form,
  * scipy.ndimage.uniform_filter, float64 central finite differences of the loss, and the
- * self-adjoint identity <box a, b> = <a, box b>.
+ * self-adjoint identity <box a, b> = <a, box b>. The float32 restatement lncc_oracle_ref32 (end of
+ * this file): the same golden vectors to float32 accuracy, exact zeros in zero and constant
+ * windows, float32-sized errors on offset intensities.
  */
 #include <math.h>
 #include <stdint.h>

@@ -6,7 +6,7 @@
 * the Python API raises the reference's exception types;
 * the fake (meta) kernels give torch.compile the right dtypes, and the loss with its backward
   traces on fake tensors;
-* the product package never imports the oracle.
+* the product package never imports the oracle, and refuses to run without the built library.
 """
 import ast
 import os
@@ -263,3 +263,22 @@ def test_product_never_imports_the_oracle():
                 if isinstance(node, (ast.Import, ast.ImportFrom)):
                     names = [a.name for a in node.names] + [getattr(node, "module", None) or ""]
                     assert not any("oracle" in n for n in names), fn
+
+
+def test_missing_library_fails_loudly():
+    """Without the built library the package refuses to run (no CPU fallback): a fresh
+    interpreter whose loader points at a path that does not exist gets an ImportError that says
+    how to build, on the first call that needs the library."""
+    import subprocess
+    import sys
+    code = ("import fused_lncc._lib as L\n"
+            "L.LIB_PATH = '/nonexistent/libfused_lncc_hip.so'\n"
+            "L._lib = None\n"
+            "try:\n"
+            "    L.load()\n"
+            "except ImportError as e:\n"
+            "    print('ImportError:', e)\n")
+    env = dict(os.environ, PYTHONPATH=os.path.join(ROOT, "fused-lncc_amd"))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert "ImportError:" in out.stdout and "no CPU fallback" in out.stdout

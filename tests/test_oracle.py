@@ -7,7 +7,10 @@
 * gradient against float64 central finite differences of the oracle's own loss, and the
   self-adjoint identity <box a, b> = <a, box b> that the backward relies on;
 * closed-form special cases (all-zero, constant pred, affine pred, NaN);
-* sensitivity: a wrong k, a wrong dr or a wrong clamp policy fails the golden comparison.
+* sensitivity: a wrong k, a wrong dr or a wrong clamp policy fails the golden comparison;
+* the float32 restatement of the reference kernel (lncc_ref32, the error yardstick of the GPU
+  numerics tests): the golden vectors to float32 accuracy, exact zeros in zero and constant
+  windows, float32-sized errors on offset intensities, and a wrong dr told apart.
 """
 import glob
 import os
@@ -255,3 +258,50 @@ def test_torch_port_matches_golden(name):
     assert abs(float(loss) - float(d["loss"])) <= 1e-6 * max(abs(float(d["loss"])), 1e-3)
     cos, rel = _cos_rel(g.numpy(), d["grad"])
     assert cos > 0.999999 and rel < 1e-5
+
+
+# ---- the float32 restatement of the reference kernel (lncc_oracle_ref32), the yardstick of the
+# GPU numerics tests: pinned here to the reference's own outputs and to exact cases
+
+@pytest.mark.parametrize("path", PARITY, ids=[os.path.basename(p)[:-4] for p in PARITY])
+def test_ref32_matches_golden(path):
+    """Same loss and gradient as the reference's torch path, to float32 accuracy."""
+    d = np.load(path)
+    loss, g = O.lncc_ref32(d["pred"], d["target"], int(d["k"]), float(d["smooth_dr"]))
+    ref = float(d["loss"])
+    assert abs(loss - ref) <= 5e-6 * max(abs(ref), 1e-3)
+    cos, rel = _cos_rel(g, d["grad"])
+    assert cos > 1 - 1e-10 and rel < 1e-5
+
+
+def test_ref32_exact_in_zero_and_constant_windows():
+    """Direct float32 window sums: a window of exact zeros, or of one representable constant per
+    input, sums exactly, so ncc and the adjoints there are exactly 0, as in float64."""
+    rng = np.random.default_rng(17)
+    p = rng.random((1, 1, 20, 11, 13)).astype(np.float32)
+    t = (0.6 * p + 0.4 * rng.random(p.shape)).astype(np.float32)
+    p[0, 0, 8:], t[0, 0, 8:] = 0.0, 0.0          # zero slab after the signal
+    p[0, 0, :, :, 7:], t[0, 0, :, :, 7:] = 0.5, 7.0   # constant block along W
+    for k in (3, 5):
+        l64, g64, maps = O.lncc(p, t, k, maps=True)
+        l32, g32, m32 = O.lncc_ref32(p, t, k, ncc_map=True)
+        zero = maps["ncc"] == 0
+        assert zero.sum() > 200 and np.all(m32[zero] == 0)
+        gz = g64 == 0
+        assert gz.sum() > 200 and np.all(g32[gz] == 0)
+        assert abs(l32 - l64) < 1e-6
+
+
+def test_ref32_rounds_in_float32():
+    """On offset intensities (100 + N(0,1)) the restatement's error against float64 is that of
+    float32 cancellation (far above float64 rounding), and a wrong dr is still told apart."""
+    rng = np.random.default_rng(3)
+    t = rng.standard_normal((1, 1, 10, 12, 12)).astype(np.float32)
+    p = (0.8 * t + 0.6 * rng.standard_normal(t.shape)).astype(np.float32)
+    l64, g64 = O.lncc(p + 100, t + 100, 5)
+    l32, g32 = O.lncc_ref32(p + 100, t + 100, 5)
+    assert 1e-6 < abs(l32 - l64) < 1e-3
+    assert 1e-5 < _cos_rel(g32, g64)[1] < 1e-2
+    d = np.load(os.path.join(GOLDEN, "dr1_k3.npz"))
+    wrong, _ = O.lncc_ref32(d["pred"], d["target"], 3, 1e-5)
+    assert abs(wrong - float(d["loss"])) > 1e-3
