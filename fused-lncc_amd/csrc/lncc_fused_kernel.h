@@ -48,22 +48,43 @@
 
 namespace fl {
 
-// Loads NV consecutive floats from a 16-byte aligned LDS address as float4s (the last one may
-// read up to 3 floats past the row; they are not used). Each float4 passes through an empty asm
-// operand that needs all four lanes, so that the loads stay 128-bit reads: otherwise the
-// optimizer re-partitions them along the box-sums' blocks (a row of 10 floats became b128 + b96 +
-// read2_b32 + b32 instead of b128 + b128 + b64), which costs LDS instructions and bank cycles.
+// Loads NV consecutive floats from a 16-byte aligned LDS address: float4s, then a tail of 2 or 1
+// floats as a float2 or a float (a tail of 3 as one more float4, which reads one float past the
+// row; it is not used), row_read(NV) floats in all. Each vector passes through an empty asm
+// operand that needs all of its lanes, so that the loads stay whole: otherwise the optimizer
+// re-partitions them along the box-sums' blocks (a row of 10 floats became b128 + b96 + read2_b32
+// + b32 instead of b128 + b128 + b64), which costs LDS instructions and bank cycles. The 2-float
+// tail (rather than a third float4) also keeps two registers per row free.
 typedef float lds_f4 __attribute__((ext_vector_type(4)));
+typedef float lds_f2 __attribute__((ext_vector_type(2)));
 template <int NV>
 __device__ __forceinline__ void lds_row(const float* __restrict__ src, float (&v)[NV]) {
+    static_assert(row_read(NV) >= NV, "row read");
 #pragma unroll
-    for (int m = 0; m < (NV + 3) / 4; ++m) {
+    for (int m = 0; m < NV / 4; ++m) {
         lds_f4 f = reinterpret_cast<const lds_f4*>(src)[m];
         asm("" : "+v"(f));
         v[4 * m] = f.x;
-        if (4 * m + 1 < NV) v[4 * m + 1] = f.y;
-        if (4 * m + 2 < NV) v[4 * m + 2] = f.z;
-        if (4 * m + 3 < NV) v[4 * m + 3] = f.w;
+        v[4 * m + 1] = f.y;
+        v[4 * m + 2] = f.z;
+        v[4 * m + 3] = f.w;
+    }
+    constexpr int t = NV / 4 * 4;
+    if constexpr (NV % 4 == 3) {
+        lds_f4 f = reinterpret_cast<const lds_f4*>(src)[NV / 4];
+        asm("" : "+v"(f));
+        v[t] = f.x;
+        v[t + 1] = f.y;
+        v[t + 2] = f.z;
+    } else if constexpr (NV % 4 == 2) {
+        lds_f2 f = *reinterpret_cast<const lds_f2*>(src + t);
+        asm("" : "+v"(f));
+        v[t] = f.x;
+        v[t + 1] = f.y;
+    } else if constexpr (NV % 4 == 1) {
+        float f = src[t];
+        asm("" : "+v"(f));
+        v[t] = f;
     }
 }
 
@@ -318,12 +339,16 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 
     // Stage order inside a phase. Each wave runs its stages in program order, so a stage placed
     // between the issue of another stage's LDS reads and their use hides part of their latency:
-    //  * P0, k <= 5: Y's rows, then F's arithmetic and prefetch, then Y's math, AYs and F's stores.
-    //    At k >= 7 the rows held across F exceed the 128-register budget of a 1024-lane workgroup
-    //    (spills): there F runs last.
+    //  * P0, k <= 5: Y's five rows are read, F's arithmetic and prefetch run while they arrive,
+    //    then Y's math, AYs, and F's stores last.
+    //  * P0, k = 7: three of Y's rows, then F whole (its z-sums stored as they are formed), then
+    //    Y's other two rows: five rows held across F, or F's z-sums held until after Y, exceed the
+    //    128-register budget of a 1024-lane workgroup (spills in the loop).
+    //  * P0, k = 9: Y, AYs, then F (its two rings leave no room for rows read early).
     //  * P1: AZ's xy-sums are read before everything else, and the unit's row is read before AZ
     //    and its sums formed after AZ.
-    constexpr bool F_EARLY = HH <= 2;
+    constexpr int Y_EARLY = HH <= 2 ? 5 : HH == 3 ? 3 : 0;   // Y rows read before F
+    constexpr bool F_STORE_AT_ONCE = Y_EARLY < 5;
 
     for (int base = zlo; base < zhi; base += K) {
         static_for<0, K>([&](auto rc) __attribute__((always_inline)) {
@@ -336,14 +361,16 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 
             // ============================ phase P0 ============================
             // Y(zi-1), AYs(zi-2), F(zi)
-            if constexpr (F_EARLY) {
+            if constexpr (Y_EARLY > 0) {
                 float yv[5][G::SY + 2 * HH];
                 if (actY && has_y) {
 #pragma unroll
-                    for (int q = 0; q < 5; ++q) lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv[q]);
+                    for (int q = 0; q < Y_EARLY; ++q) lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv[q]);
                 }
-                f_sums(rc, std::false_type{}, zi, zoff);
+                f_sums(rc, std::integral_constant<bool, F_STORE_AT_ONCE>{}, zi, zoff);
                 if (actY && has_y) {
+#pragma unroll
+                    for (int q = Y_EARLY; q < 5; ++q) lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv[q]);
                     float S[5][G::SY];
 #pragma unroll
                     for (int q = 0; q < 5; ++q) box_sums<HH, G::SY>(yv[q], S[q]);
@@ -370,10 +397,10 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     for (int i = 0; i < G::SB; ++i) GY[b_dst + i * G::GYS] = o[i];
                 }
             }
-            if constexpr (F_EARLY) {
-                f_store();
-            } else {
+            if constexpr (Y_EARLY == 0) {
                 f_sums(rc, std::true_type{}, zi, zoff);
+            } else if constexpr (!F_STORE_AT_ONCE) {
+                f_store();
             }
             __syncthreads();
 

@@ -30,6 +30,9 @@ constexpr int odd(int a) { return a | 1; }
 constexpr int stride4(int n) { return n + ((12 - n % 8) % 8); }
 constexpr int rup4(int n) { return (n + 3) / 4 * 4; }
 constexpr int rup64(int n) { return (n + 63) / 64 * 64; }
+// Floats fetched by the LDS read of a row of n values: float4 pieces, and a tail of 2 or 1 values
+// as a float2 or a float (a tail of 3 as one more float4).
+FL_HD constexpr int row_read(int n) { return n % 4 == 3 ? rup4(n) : n; }
 
 // Tile geometry for halo H (k = 2H+1). Coordinates inside a workgroup:
 //   input region   ix in [0,IX), iy in [0,IY)  <-> global (x0-2H+ix, y0-2H+iy)
@@ -76,10 +79,10 @@ struct Geo {
     static constexpr int ZS = stride4(IX), XS = stride4(cmax(IY, AY)), GS = stride4(AX), GXS = XS;
     static constexpr int GYS = TX + 1, PAD = 16;
     static constexpr int ZP = IY * ZS, XP = XR * XS, GP = YR * GS, GXP = TX * GXS, GYP = TY * GYS;
-    // A segment reads rup4(S + 2H) floats from its start; reads past a row's end stay inside the
-    // buffer (the next row or the spare floats) and only feed outputs that are never used.
-    static_assert(SX + rup4(SX + 2 * H) <= ZS + PAD && YR - SY + rup4(SY + 2 * H) <= XS + PAD &&
-                      TX - SA + rup4(SA + 2 * H) <= GS + PAD && TY - SB + rup4(SB + 2 * H) <= GXS + PAD,
+    // A segment reads row_read(S + 2H) floats from its start; reads past a row's end stay inside
+    // the buffer (the next row or the spare floats) and only feed outputs that are never used.
+    static_assert(SX + row_read(SX + 2 * H) <= ZS + PAD && YR - SY + row_read(SY + 2 * H) <= XS + PAD &&
+                      TX - SA + row_read(SA + 2 * H) <= GS + PAD && TY - SB + row_read(SB + 2 * H) <= GXS + PAD,
                   "row reads");
     static constexpr int LDS_FLOATS = 5 * (ZP + XP) + 3 * (GP + GXP + GYP) + 4 * PAD;
     static_assert(LDS_FLOATS * 4 <= 160 * 1024, "LDS");

@@ -79,10 +79,10 @@ long check(int plant) {
         m.writes[p].resize(NARR);
         for (int a = 0; a < NARR; ++a) m.writes[p][a].assign(m.size[a], 0);
     }
-    const int rows_x = fl::rup4(G::SX + 2 * H);                       // X row read (floats)
-    const int rows_a = fl::rup4(G::SX + 2 * H);  // AX row read: the unit row is read as an X row
-    const int rows_y = fl::rup4(G::SY + 2 * H) - (plant == 2 ? 1 : 0);
-    const int rows_b = fl::rup4(G::SB + 2 * H);
+    const int rows_x = fl::row_read(G::SX + 2 * H);                       // X row read (floats)
+    const int rows_a = fl::row_read(G::SX + 2 * H);  // AX row read: the unit row is read as an X row
+    const int rows_y = fl::row_read(G::SY + 2 * H) - (plant == 2 ? 1 : 0);
+    const int rows_b = fl::row_read(G::SB + 2 * H);
 
     // ---- writes of both phases first (each phase's reads use the other phase's writes)
     for (int tid = 0; tid < fl::NT; ++tid) {
