@@ -107,6 +107,12 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     __shared__ double red[NT / 64];
 
     const int tid = threadIdx.x;
+    // the wave's index in the workgroup, wave-uniform (a scalar register): at k >= 7 the reduction
+    // after the march uses it with the lane index (recomputed there), so that no vector register
+    // carries the thread index across the march (at the register limit of those kernels it was
+    // spilled to scratch: 6 MB of extra HBM traffic per launch at (2,16,128^3)); at k <= 5, where
+    // nothing spills, keeping the thread index measured 1% faster
+    const int wave_id = __builtin_amdgcn_readfirstlane(tid) >> 6;
     const int D = a.dimD, Hd = a.dimH, Wd = a.dimW;
 
     // workgroup -> tile. Workgroups go to the 8 XCDs round-robin (workgroup i on XCD i % 8); XCD j
@@ -452,9 +458,11 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     if constexpr (MODE == MODE_MAPS) return;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) loss_acc += __shfl_xor(loss_acc, off, 64);
-    if ((tid & 63) == 0) red[tid >> 6] = loss_acc;
+    const int lane = HH >= 3 ? (int)__lane_id() : (tid & 63);
+    const int wave = HH >= 3 ? wave_id : (tid >> 6);
+    if (lane == 0) red[wave] = loss_acc;
     __syncthreads();
-    if (tid == 0) {
+    if (wave == 0 && lane == 0) {
         double sum = 0.0;
 #pragma unroll
         for (int w = 0; w < NT / 64; ++w) sum += red[w];
