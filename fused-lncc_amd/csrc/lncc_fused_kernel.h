@@ -415,7 +415,12 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             float ys[3];
             if constexpr (ADJ) {
 #pragma unroll
-                for (int c = 0; c < 3; ++c) ys[c] = actB ? GY[c * G::GYP + z_oy * G::GYS + z_ox] : 0.f;
+                for (int c = 0; c < 3; ++c) {
+                    // read whatever actB says (the value is dropped when it is false), so that the
+                    // three reads pair up
+                    const float gy = GY[c * G::GYP + z_oy * G::GYS + z_ox];
+                    ys[c] = actB ? gy : 0.f;
+                }
             }
             const int zcX = zi - HH;
             const bool actX = zcX >= zc_lo && zcX < zc_hi;
