@@ -146,6 +146,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             if (gx >= 0 && gx < Wd && gy >= 0 && gy < Hd) voff[j] = (uint32_t)((gy * Wd + gx) * ELEM);
         }
     }
+    if constexpr (G::FPAIR) zaddr[1] = zaddr[0] + NT;  // a lane without a second column writes padding
     // P1 units: X (z-sums -> x-sums) then AX (adjoints -> x-sums); offsets into the source and
     // destination buffers and the unit kind (0 none, 1 X, 2 AX)
     int u_src[G::U1], u_dst[G::U1], u_kind[G::U1];
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
         for (int j = 0; j < J; ++j) {
             zstep5<K, r>(pnext[j], tnext[j], fpre[j], pring[j], tring[j], zsum[j]);
             if constexpr (STORE) {
-                if (zaddr[j] >= 0) {
+                if (G::FPAIR || zaddr[j] >= 0) {
 #pragma unroll
                     for (int q = 0; q < 5; ++q) Zs[q * G::ZP + zaddr[j]] = zsum[j][q];
                 }

@@ -80,9 +80,13 @@ struct Geo {
     static constexpr int GYS = TX + 1, PAD = 16;
     // The planes F writes (one column, five fields) and AZ reads (one column, three fields) are a
     // multiple of 64 floats apart for k >= 5, so that those accesses pair into write2st64 /
-    // read2st64 (6 LDS instructions per lane and step instead of 10 for F, 2 instead of 3 for AZ;
-    // 2-4% faster at k = 5..9, k = 3 measured 0.6% slower with it)
-    static constexpr int ZP = H >= 2 ? rup64(IY * ZS) : IY * ZS, XP = XR * XS, GP = YR * GS, GXP = TX * GXS,
+    // read2st64 (6 LDS instructions per lane and step instead of 10 for F, 5 with FPAIR; 2 instead
+    // of 3 for AZ; 2-4% faster at k = 5..9, k = 3 measured 0.6% slower with it)
+    // k = 7: a lane's two F columns are NT floats apart in every Zs plane (ZS == IX), planes of
+    // 2 NT floats: a lane without a second column writes its (zero) z-sums into the padding, so
+    // that every lane's ten z-sum stores pair into five write2st64
+    static constexpr bool FPAIR = (H == 3 && ZS == IX && J == 2);
+    static constexpr int ZP = FPAIR ? 2 * NT : H >= 2 ? rup64(IY * ZS) : IY * ZS, XP = XR * XS, GP = YR * GS, GXP = TX * GXS,
                          GYP = H >= 2 ? rup64(TY * GYS) : TY * GYS;
     // A segment reads row_read(S + 2H) floats from its start; reads past a row's end stay inside
     // the buffer (the next row or the spare floats) and only feed outputs that are never used.

@@ -89,7 +89,14 @@ long check(int plant) {
         // P0 / F: the five z-sums of each input column
         for (int j = 0; j < G::J; ++j) {
             int ix, iy, zaddr;
-            if (!fl::f_column<G>(tid + j * fl::NT, ix, iy, zaddr)) continue;
+            if (!fl::f_column<G>(tid + j * fl::NT, ix, iy, zaddr)) {
+                if (!G::FPAIR) continue;
+                // paired stores: a lane without this column writes zeros into the plane padding
+                int ix0, iy0;
+                fl::f_column<G>(tid, ix0, iy0, zaddr);
+                zaddr += j * fl::NT;
+                if (zaddr < G::IY * G::ZS) m.fail("F padding write inside the plane");
+            }
             if (plant == 1) zaddr += 1;
             for (int q = 0; q < 5; ++q) m.write(0, ZS, (long)q * G::ZP + zaddr);
         }
