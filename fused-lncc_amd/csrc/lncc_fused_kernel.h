@@ -28,7 +28,8 @@
 //
 // Software pipeline: the chain F -> X -> Y -> AX -> AYs -> AZ alternates between two phases per
 // plane, P0 = {F(zi), Y(zi-1), AYs(zi-2)} and P1 = {X(zi), AX(zi-1), AZ(zi-2)}, so each plane costs
-// two workgroup barriers, and the stages that share a phase run on disjoint waves.
+// two workgroup barriers. F and AZ run on every lane; the Y items and the AYs units, and the X and
+// the AX units, sit on disjoint waves.
 //
 // Reference semantics (fused_lncc/csrc/lncc3d.cu:93-107, baselines/torch_lncc.py:25-32):
 //   cross = Spt - Sp St/n ; vp = max(Spp - Sp^2/n, 0) + dr ; vt likewise ; ncc = cross^2/(vp vt);
@@ -243,6 +244,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     auto y_math = [&](const float (&S)[5][G::SY], int zcY) __attribute__((always_inline)) {
         const bool count = zcY >= z0 && zcY < z1;
         float lsum = -0.f;  // -0 + x == x for every x, so the first add folds away
+        float adj[3][G::SY];  // alpha, beta, gamma of the segment's outputs
 #pragma unroll
         for (int i = 0; i < G::SY; ++i) {
             const int ay = y_start + i;
@@ -264,9 +266,15 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 const float crm = live ? cr : 0.f;
                 const float uu = crm * VT;
                 const float w = fmaf(-Sp, uu, St);
-                Gs[0 * G::GP + ay * G::GS + y_ax] = crm * w;
-                Gs[1 * G::GP + ay * G::GS + y_ax] = crm * uu;
-                Gs[2 * G::GP + ay * G::GS + y_ax] = crm;
+                if constexpr (G::ASWAP) {
+                    adj[0][i] = crm * w;
+                    adj[1][i] = crm * uu;
+                    adj[2][i] = crm;
+                } else {
+                    Gs[y_gs<G>(0, y_ax, ay)] = crm * w;
+                    Gs[y_gs<G>(1, y_ax, ay)] = crm * uu;
+                    Gs[y_gs<G>(2, y_ax, ay)] = crm;
+                }
             }
             if constexpr (MODE == MODE_MAPS) {
                 if (count && y_core[i]) {
@@ -282,6 +290,12 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     }
                 }
             }
+        }
+        if constexpr (ADJ && G::ASWAP) {  // Gs rows along y: one float4 per field
+            static_assert(G::SY == 4, "float4 rows");
+#pragma unroll
+            for (int c = 0; c < 3; ++c)
+                *reinterpret_cast<lds_f4*>(Gs + y_gs<G>(c, y_ax, y_start)) = lds_f4{adj[c][0], adj[c][1], adj[c][2], adj[c][3]};
         }
         loss_acc += (double)lsum;
     };
@@ -395,13 +409,21 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 y_math(S, zcY);
             }
             if constexpr (ADJ) {
-                // AYs(zi-2): y-sums of alpha, beta, gamma at plane zcB (one quantity per unit)
+                // AYs(zi-2): y-sums (x-sums with ASWAP) of alpha, beta, gamma at plane zcB (one
+                // quantity per unit)
                 if (actB && has_b) {
                     float v[G::SB + 2 * HH], o[G::SB];
                     lds_row(GXs + b_src, v);
                     box_sums<HH, G::SB>(v, o);
 #pragma unroll
-                    for (int i = 0; i < G::SB; ++i) GY[b_dst + i * G::GYS] = o[i];
+                    for (int i = 0; i < G::SB; ++i) {
+                        if constexpr (G::ASWAP) {  // GY rows along x: float4s
+                            if (i % 4 == 0)
+                                *reinterpret_cast<lds_f4*>(GY + b_dst + i) = lds_f4{o[i], o[i + 1], o[i + 2], o[i + 3]};
+                        } else {
+                            GY[b_dst + i * G::BW] = o[i];
+                        }
+                    }
                 }
             }
             if constexpr (Y_EARLY == 0) {

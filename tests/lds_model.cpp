@@ -105,12 +105,12 @@ long check(int plant) {
             int seg, ax;
             fl::y_item<G>(tid, seg, ax);
             for (int c = 0; c < NA; ++c)
-                for (int i = 0; i < G::SY; ++i) m.write(0, GS, (long)c * G::GP + (seg * G::SY + i) * G::GS + ax);
+                for (int i = 0; i < G::SY; ++i) m.write(0, GS, fl::y_gs<G>(c, ax, seg * G::SY + i));
         }
         // P0 / AYs
         int bsrc, bdst;
         if (fl::ays_unit<G>(tid, bsrc, bdst))
-            for (int i = 0; i < G::SB; ++i) m.write(0, GY, bdst + (long)i * (G::GYS - (plant == 3 ? 1 : 0)));
+            for (int i = 0; i < G::SB; ++i) m.write(0, GY, bdst + (long)i * (G::BW - (plant == 3 ? 1 : 0)));
         // P1 / X and AX
         int src, dst;
         const int kind = fl::p1_unit<G, true>(tid, src, dst);
