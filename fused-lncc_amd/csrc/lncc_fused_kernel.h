@@ -27,9 +27,13 @@
 // rounding of every earlier plane into them.
 //
 // Software pipeline: the chain F -> X -> Y -> AX -> AYs -> AZ alternates between two phases per
-// plane, P0 = {F(zi), Y(zi-1), AYs(zi-2)} and P1 = {X(zi), AX(zi-1), AZ(zi-2)}, so each plane costs
-// two workgroup barriers. F and AZ run on every lane; the Y items and the AYs units, and the X and
-// the AX units, sit on disjoint waves.
+// plane, so each plane costs two workgroup barriers and every LDS buffer is written in one phase
+// and read in the other:
+//   P0 = {F(zi), Y(zi-1) y-sums, AX(zi-2), AZ(zi-3)}   P1 = {X(zi), Y(zi-1) ncc, AYs(zi-2)}
+// Y is split over the phases: its y-sums (LDS reads of Xs) in P0, its ncc and adjoint arithmetic
+// (the largest block of VALU work, registers only) in P1, where it runs while the X and AYs units
+// wait for their LDS rows. F and AZ run on every lane; the Y items, the X units, the AX units and
+// the AYs units sit on waves chosen per phase so that no lane holds two kinds of row at once.
 //
 // Reference semantics (fused_lncc/csrc/lncc3d.cu:93-107, baselines/torch_lncc.py:25-32):
 //   cross = Spt - Sp St/n ; vp = max(Spp - Sp^2/n, 0) + dr ; vt likewise ; ncc = cross^2/(vp vt);
@@ -148,12 +152,17 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
         }
     }
     if constexpr (G::FPAIR) zaddr[1] = zaddr[0] + NT;  // a lane without a second column writes padding
-    // P1 units: X (z-sums -> x-sums) then AX (adjoints -> x-sums); offsets into the source and
-    // destination buffers and the unit kind (0 none, 1 X, 2 AX)
-    int u_src[G::U1], u_dst[G::U1], u_kind[G::U1];
-#pragma unroll
-    for (int k = 0; k < G::U1; ++k) u_kind[k] = p1_unit<G, ADJ>(tid + k * NT, u_src[k], u_dst[k]);
-    // P0: Y items on lanes [0, YITEMS), AYs units on waves 10, 11, 14, 15
+    // Y items on lanes [0, YITEMS) (y-sums in P0, ncc arithmetic in P1), X and AYs units in P1,
+    // AX units in P0 (lncc_geometry.h); offsets into the source and destination buffers
+    // (a lane has at most one P1 unit, X or AYs, so the two share one pair of offsets)
+    int u_src, u_dst, a_src, a_dst, b_src, b_dst;
+    const bool has_x = x_unit<G>(tid, u_src, u_dst);
+    const bool has_a = ax_unit<G>(tid, a_src, a_dst) && ADJ;
+    const bool has_b = ays_unit<G>(tid, b_src, b_dst) && ADJ;
+    if (has_b) {
+        u_src = b_src;
+        u_dst = b_dst;
+    }
     const bool has_y = tid < G::YITEMS;
     int y_seg = 0, y_ax = 0;  // rows seg of AX positions
     if (has_y) y_item<G>(tid, y_seg, y_ax);
@@ -172,8 +181,6 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             y_core[i] = y_inv[i] && corex && ay >= HH && ay < HH + TY;
         }
     }
-    int b_src, b_dst;
-    const bool has_b = ays_unit<G>(tid, b_src, b_dst) && ADJ;
     const bool has_z = ADJ && tid < G::NOUT;
     int z_ox, z_oy;
     az_lane<G>(tid, z_ox, z_oy);
@@ -182,7 +189,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 
     constexpr int LEAD = ADJ ? 2 * HH : HH;
     const int zlo = max(z0 - LEAD, 0);
-    const int zhi = ADJ ? z1 + 2 + 2 * HH : z1 + 1 + HH;
+    const int zhi = ADJ ? z1 + 3 + 2 * HH : z1 + 1 + HH;
     const int zc_lo = ADJ ? max(z0 - HH, 0) : z0;
     const int zc_hi = ADJ ? min(z1 + HH, D) : z1;
 
@@ -190,13 +197,14 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // k), the prefix sums of the five fields over the current block, and p,t of the next plane
     // (prefetched one step ahead). The ring starts at zero: nothing before the first plane of the
     // march enters a window that is used.
-    float pring[J][K], tring[J][K], fpre[J][5], zsum[J][5], pnext[J], tnext[J];
+    float pring[J][K], tring[J][K], fpre[J][5], fch[J][5], zsum[J][5], pnext[J], tnext[J];
     float pz = 0.f, tzz = 0.f;  // AZ: p,t at this step's output plane (prefetched one step ahead)
 #pragma unroll
     for (int j = 0; j < J; ++j) {
 #pragma unroll
         for (int q = 0; q < 5; ++q) {
             fpre[j][q] = 0.f;
+            fch[j][q] = 0.f;
             zsum[j][q] = 0.f;
         }
 #pragma unroll
@@ -235,7 +243,11 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const uint64_t gva = (uint64_t)(uintptr_t)gvol;
     uint64_t zoff = (uint64_t)zlo * PB;
     const int zn_hi = min(zhi, D);                 // F: new plane zi+1 valid while zi+1 < zn_hi
-    constexpr int ZO = 2 + 2 * HH;                 // AZ: output plane zi-ZO
+    constexpr int ZO = 3 + 2 * HH;                 // AZ: output plane zi-ZO
+    // z-window chains (zstep5 / zstep1): the previous block's sums over ring slots F_CHAIN..K-1
+    // (F) and A_CHAIN..K-1 (AZ) kept as partial sums; 0 = none
+    constexpr int F_CHAIN = HH == 3 ? 4 : 0;
+    constexpr int A_CHAIN = HH >= 2 && HH <= 3 ? HH + 1 : 0;
 
     // Stage bodies; the march below orders them per phase.
     //
@@ -310,7 +322,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
         constexpr bool STORE = decltype(store)::value;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            zstep5<K, r>(pnext[j], tnext[j], fpre[j], pring[j], tring[j], zsum[j]);
+            zstep5<K, r, F_CHAIN>(pnext[j], tnext[j], fpre[j], pring[j], tring[j], fch[j], zsum[j]);
             if constexpr (STORE) {
                 if (G::FPAIR || zaddr[j] >= 0) {
 #pragma unroll
@@ -337,133 +349,111 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             }
         }
     };
-    // X(zi) or AX(zi-1), the lane's unit: x-sums of one z-sum (feeds Y at the next plane) or of
-    // one of alpha, beta, gamma at plane zcY, over one segment. The row is read early and the sums
-    // formed by u_math later; the early read takes SX + 2h floats for both kinds (SX >= SA), and an
-    // AX row's extra floats stay inside Gs, unused.
-    static_assert(G::U1 == 1 && G::SX >= G::SA, "one unit per lane");
-    auto u_math = [&](const float (&uv)[G::SX + 2 * HH], bool runX, bool runA) __attribute__((always_inline)) {
-        if (runX) {
-            float o[G::SX];
-            box_sums<HH, G::SX>(uv, o);
-#pragma unroll
-            for (int i = 0; i < G::SX; ++i) Xs[u_dst[0] + i * G::XS] = o[i];
-        } else if (runA) {
-            float v[G::SA + 2 * HH], o[G::SA];
-#pragma unroll
-            for (int i = 0; i < G::SA + 2 * HH; ++i) v[i] = uv[i];
-            box_sums<HH, G::SA>(v, o);
-#pragma unroll
-            for (int i = 0; i < G::SA; ++i) GXs[u_dst[0] + i * G::GXS] = o[i];
-        }
-    };
-
     // Stage order inside a phase. Each wave runs its stages in program order, so a stage placed
-    // between the issue of another stage's LDS reads and their use hides part of their latency:
-    //  * P0, k <= 5: Y's five rows are read, F's arithmetic and prefetch run while they arrive,
-    //    then Y's math, AYs, and F's stores last.
-    //  * P0, k = 7: three of Y's rows, then F whole (its z-sums stored as they are formed), then
-    //    Y's other two rows: five rows held across F, or F's z-sums held until after Y, exceed the
-    //    128-register budget of a 1024-lane workgroup (spills in the loop).
-    //  * P0, k = 9: Y, AYs, then F (its two rings leave no room for rows read early).
-    //  * P1: AZ's xy-sums are read before everything else, and the unit's row is read before AZ
-    //    and its sums formed after AZ.
-    constexpr int Y_EARLY = HH <= 2 ? 5 : HH == 3 ? 3 : 0;   // Y rows read before F
+    // between the issue of another stage's LDS reads and their use hides part of their latency.
+    //  * P0: AZ's xy-sums are read first. The Y lanes read Y_EARLY of their five rows (all five
+    //    at k <= 5, one at k = 7: more rows held across F exceed the 128-register budget of a
+    //    1024-lane workgroup) and at k <= 5 the AX lanes their row, F runs while they arrive, then
+    //    the Y lanes read their other rows and form the five box sums, which stay in registers
+    //    until P1, and the AX lanes their sums; AZ's z-sums and the gradient come last. At k = 9
+    //    (two rings of 9 planes) nothing is read early and Y's rows are read one at a time. (At
+    //    k = 7 the AX row read before F measured 1% slower than after it.)
+    //  * P1: the Y lanes turn their box sums into ncc and the adjoint coefficients (arithmetic
+    //    only, no LDS reads: it keeps the SIMDs busy while the rows of the X and AYs units, on the
+    //    other waves, arrive), then the X and AYs units.
+    constexpr int Y_EARLY = HH <= 2 ? 5 : HH == 3 ? 1 : 0;   // Y rows read before F
     constexpr bool F_STORE_AT_ONCE = Y_EARLY < 5;
+    constexpr bool AX_EARLY = HH <= 2;                        // the AX row read before F
+    constexpr int NY = G::SY + 2 * HH, NA = G::SA + 2 * HH, NX = G::SX + 2 * HH, NB = G::SB + 2 * HH;
+    // P0's early reads (Y's first rows or the AX row) share one register array: the two kinds of
+    // lane sit on different waves
+    constexpr int NE0 = cmax(cmax(Y_EARLY * NY, AX_EARLY ? NA : 0), NY);
 
     for (int base = zlo; base < zhi; base += K) {
         static_for<0, K>([&](auto rc) __attribute__((always_inline)) {
             const int zi = base + decltype(rc)::value;
             if (zi >= zhi) return;
-            const int zcY = zi - 1 - HH;   // Y(zi-1) and AX(zi-1)
+            const int zcX = zi - HH;       // X(zi): the z-sums of F(zi) are centred on plane zi-h
+            const bool actX = zcX >= zc_lo && zcX < zc_hi;
+            const int zcY = zi - 1 - HH;   // Y(zi-1)
             const bool actY = zcY >= zc_lo && zcY < zc_hi;
-            const int zcB = zi - 2 - HH;   // AYs(zi-2) and the xy-sums AZ(zi-2) reads
+            const int zcB = zi - 2 - HH;   // AX(zi-2) and AYs(zi-2)
             const bool actB = ADJ && zcB >= zc_lo && zcB < zc_hi;
+            const int zcA = zi - 3 - HH;   // the xy-sums AZ(zi-3) reads
+            const bool actA = ADJ && zcA >= zc_lo && zcA < zc_hi;
 
             // ============================ phase P0 ============================
-            // Y(zi-1), AYs(zi-2), F(zi)
-            if constexpr (Y_EARLY > 0) {
-                float yv[5][G::SY + 2 * HH];
-                if (actY && has_y) {
-#pragma unroll
-                    for (int q = 0; q < Y_EARLY; ++q) lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv[q]);
-                }
-                f_sums(rc, std::integral_constant<bool, F_STORE_AT_ONCE>{}, zi, zoff);
-                if (actY && has_y) {
-#pragma unroll
-                    for (int q = Y_EARLY; q < 5; ++q) lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv[q]);
-                    float S[5][G::SY];
-#pragma unroll
-                    for (int q = 0; q < 5; ++q) box_sums<HH, G::SY>(yv[q], S[q]);
-                    y_math(S, zcY);
-                }
-            } else if (actY && has_y) {
-                // one row at a time: all five held at once exceed the register budget here
-                float S[5][G::SY];
-#pragma unroll
-                for (int q = 0; q < 5; ++q) {
-                    float yv[G::SY + 2 * HH];
-                    lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, yv);
-                    box_sums<HH, G::SY>(yv, S[q]);
-                }
-                y_math(S, zcY);
-            }
-            if constexpr (ADJ) {
-                // AYs(zi-2): y-sums (x-sums with ASWAP) of alpha, beta, gamma at plane zcB (one
-                // quantity per unit)
-                if (actB && has_b) {
-                    float v[G::SB + 2 * HH], o[G::SB];
-                    lds_row(GXs + b_src, v);
-                    box_sums<HH, G::SB>(v, o);
-#pragma unroll
-                    for (int i = 0; i < G::SB; ++i) {
-                        if constexpr (G::ASWAP) {  // GY rows along x: float4s
-                            if (i % 4 == 0)
-                                *reinterpret_cast<lds_f4*>(GY + b_dst + i) = lds_f4{o[i], o[i + 1], o[i + 2], o[i + 3]};
-                        } else {
-                            GY[b_dst + i * G::BW] = o[i];
-                        }
-                    }
-                }
-            }
-            if constexpr (Y_EARLY == 0) {
-                f_sums(rc, std::true_type{}, zi, zoff);
-            } else if constexpr (!F_STORE_AT_ONCE) {
-                f_store();
-            }
-            __syncthreads();
-
-            // ============================ phase P1 ============================
-            // X(zi) and AX(zi-1) on the unit lanes, AZ(zi-2) on the output lanes
+            // AZ(zi-3) reads, Y(zi-1) y-sums, AX(zi-2), F(zi), AZ(zi-3)
+            // AZ's xy-sums: read first, except at k = 9, where they would be held across F
             float ys[3];
-            if constexpr (ADJ) {
+            auto az_read = [&]() __attribute__((always_inline)) {
 #pragma unroll
                 for (int c = 0; c < 3; ++c) {
-                    // read whatever actB says (the value is dropped when it is false), so that the
+                    // read whatever actA says (the value is dropped when it is false), so that the
                     // three reads pair up
                     const float gy = GY[c * G::GYP + z_oy * G::GYS + z_ox];
-                    ys[c] = actB ? gy : 0.f;
+                    ys[c] = actA ? gy : 0.f;
                 }
+            };
+            if constexpr (ADJ && HH <= 3) az_read();
+            float er[NE0];
+            if (has_y && actY) {
+#pragma unroll
+                for (int q = 0; q < Y_EARLY; ++q) {
+                    float v[NY];
+                    lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, v);
+#pragma unroll
+                    for (int i = 0; i < NY; ++i) er[q * NY + i] = v[i];
+                }
+            } else if (AX_EARLY && has_a && actB) {
+                float v[NA];
+                lds_row(Gs + a_src, v);
+#pragma unroll
+                for (int i = 0; i < NA; ++i) er[i] = v[i];
             }
-            const int zcX = zi - HH;
-            const bool actX = zcX >= zc_lo && zcX < zc_hi;
-            const bool runX = u_kind[0] == 1 && actX, runA = ADJ && u_kind[0] == 2 && actY;
-            float uv[G::SX + 2 * HH];
-            if (runX || runA) lds_row((runA ? Gs : Zs) + u_src[0], uv);
+            f_sums(rc, std::integral_constant<bool, F_STORE_AT_ONCE>{}, zi, zoff);
+            float S[5][G::SY];  // Y's box sums, carried into P1
+            if (has_y && actY) {
+#pragma unroll
+                for (int q = 0; q < 5; ++q) {
+                    float v[NY];
+                    if (q < Y_EARLY) {
+#pragma unroll
+                        for (int i = 0; i < NY; ++i) v[i] = er[(q < Y_EARLY ? q : 0) * NY + i];
+                    } else {
+                        lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, v);
+                    }
+                    box_sums<HH, G::SY>(v, S[q]);
+                }
+            } else if (has_a && actB) {
+                // AX(zi-2): x-sums (y-sums with ASWAP) of one of alpha, beta, gamma over one segment
+                float v[NA], o[G::SA];
+                if constexpr (AX_EARLY) {
+#pragma unroll
+                    for (int i = 0; i < NA; ++i) v[i] = er[i];
+                } else {
+                    lds_row(Gs + a_src, v);
+                }
+                box_sums<HH, G::SA>(v, o);
+#pragma unroll
+                for (int i = 0; i < G::SA; ++i) GXs[a_dst + i * G::GXS] = o[i];
+            }
+            if constexpr (!F_STORE_AT_ONCE) f_store();
+            if constexpr (ADJ && HH > 3) az_read();
             if constexpr (ADJ) {
-                // AZ(zi-2): z-sums of the xy-sums over the k planes of the output plane zo = the
-                // prefix of the current block plus the previous block's suffix still in the ring
+                // AZ(zi-3): z-sums of the xy-sums over the k planes of the output plane zo = the
+                // prefix of the current block plus the previous block's suffix (ring and chain)
                 // (lanes without an output column run on a clamped one and store out of range,
                 // i.e. nothing)
                 constexpr int r = decltype(rc)::value;
                 float gw[3];
 #pragma unroll
-                for (int c = 0; c < 3; ++c) gw[c] = zstep1<K, r>(ys[c], gpre[c], gring[c]);
+                for (int c = 0; c < 3; ++c) gw[c] = zstep1<K, r, A_CHAIN>(ys[c], gpre[c], gring[c]);
                 const int zo = zi - ZO;
                 const float g = a.gscale * fmaf(inv_n, gw[0], fmaf(pz, gw[1], -tzz * gw[2]));
                 // Non-temporal: the gradient is never read back, and this re-read of p,t is the
                 // last use of those lines. With the default policy both would be promoted in the
-                // L2 and push out the planes that F loaded and this stage re-reads 2h+2 steps
+                // L2 and push out the planes that F loaded and this stage re-reads 2h+3 steps
                 // later, so that every input byte would be fetched about twice; marked
                 // evict-first, every input byte is fetched from HBM once. bf16 gradient rows of a
                 // tile are half a 128-byte line (the x-neighbour tile writes the other half):
@@ -476,7 +466,33 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 pz = load_elem<BF16, kNT>(rsrc_at(pva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
                 tzz = load_elem<BF16, kNT>(rsrc_at(tva + zoff - (ZO - 1) * PB, plane_bytes, oko), z_voff);
             }
-            u_math(uv, runX, runA);
+            __syncthreads();
+
+            // ============================ phase P1 ============================
+            // Y(zi-1) ncc arithmetic, X(zi), AYs(zi-2)
+            if (has_y && actY) y_math(S, zcY);
+            if (has_x && actX) {
+                // X(zi): x-sums of one of the five z-sums over one segment (feeds Y at the next plane)
+                float v[NX], o[G::SX];
+                lds_row(Zs + u_src, v);
+                box_sums<HH, G::SX>(v, o);
+#pragma unroll
+                for (int i = 0; i < G::SX; ++i) Xs[u_dst + i * G::XS] = o[i];
+            } else if (has_b && actB) {
+                // AYs(zi-2): y-sums (x-sums with ASWAP) of one of alpha, beta, gamma at plane zcB
+                float v[NB], o[G::SB];
+                lds_row(GXs + u_src, v);
+                box_sums<HH, G::SB>(v, o);
+#pragma unroll
+                for (int i = 0; i < G::SB; ++i) {
+                    if constexpr (G::ASWAP) {  // GY rows along x: float4s
+                        if (i % 4 == 0)
+                            *reinterpret_cast<lds_f4*>(GY + u_dst + i) = lds_f4{o[i], o[i + 1], o[i + 2], o[i + 3]};
+                    } else {
+                        GY[u_dst + i * G::BW] = o[i];
+                    }
+                }
+            }
             zoff += PB;
             __syncthreads();
         });

@@ -56,9 +56,9 @@ struct Geo {
     static constexpr int SX = rup4(cdiv(AX, 2)), XSEG = 2, XR = XSEG * SX, XITEMS = IY * XSEG;
     // Y: y-sums -> box sums, ncc, adjoints; items (ax, seg), outputs ay < YR (>= AY)
     static constexpr int SY = 4, YSEG = cdiv(AY, SY), YR = YSEG * SY, YITEMS = AX * YSEG;
-    // Adjoint passes: AX (phase P1) box-sums alpha, beta, gamma along x, AYs (phase P0) along y.
-    // At k = 7 (ASWAP) the order is swapped, y in P1 and x in P0: the rows of Gs then run along y,
-    // so Y stores the four outputs of a field as one float4, and the rows of GY along x, so AYs
+    // Adjoint passes: AX (phase P0) box-sums alpha, beta, gamma along x, AYs (phase P1) along y.
+    // At k = 7 (ASWAP) the order is swapped, y first and x second: the rows of Gs then run along
+    // y, so Y stores the four outputs of a field as one float4, and the rows of GY along x, so AYs
     // stores its 16 outputs as four float4s (34 LDS store instructions fewer per plane than the
     // scattered 32-bit stores; measured 1.2% faster at k = 7, 0.4-0.7% slower at k = 3, 5, 5%
     // slower at k = 9).
@@ -70,16 +70,16 @@ struct Geo {
     // AYs: items (pos, seg), pos over the TX columns (y-sums, outputs oy < TY) or, with ASWAP,
     // over the TY rows (x-sums, outputs ox < TX); BW = the stride of its outputs in GY
     static constexpr int SB = (ASWAP ? TX : TY) / 2, BSEG = 2, BPOS = ASWAP ? TY : TX, BITEMS = BPOS * BSEG;
-    // Work units of the box-sum passes are single quantities of one segment. Waves are spread
-    // over the 4 SIMDs of the CU round-robin (wave w on SIMD w % 4), so the heavy items are placed
-    // to even out each SIMD's share of a phase: in phase P1 the X units (5 per item) fill the
-    // first waves and the AX units (3 per item) start on the next wave boundary; in phase P0 the
-    // Y items fill the first waves (SIMDs 0 and 1 get the extra ones) and the AYs units (3 per
-    // item) go to waves 10, 11, 14, 15 (SIMDs 2 and 3), B_PER_WAVE each.
-    static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, AX_LANE0 = rup64(UX), U1 = 1;
-    static constexpr int UB = 3 * BITEMS, B_PER_WAVE = UB / 4;
-    static_assert(YITEMS <= 10 * 64 && AX_LANE0 + UA <= NT && BPOS == 32 && TX == 32 && UB == 192 &&
-                      B_PER_WAVE == 48 && NIN <= 2 * NT && TY <= TY_MAX,
+    // Work units of the box-sum passes are single quantities of one segment. Lanes by phase:
+    //   P0  Y's y-sums on lanes [0, YITEMS); AX units on the NAW waves ax_wave(0..NAW-1), 64 each
+    //   P1  Y's ncc arithmetic on the same lanes; X units on [XL0, XL0 + UX); AYs units on
+    //       [BL0, BL0 + UB)
+    // (F and AZ run on every lane in P0.) Waves sit on the CU's 4 SIMDs round-robin (wave w on
+    // SIMD w % 4): the AX waves go to the SIMDs with fewer Y waves, which evens out P0.
+    static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, UB = 3 * BITEMS;
+    static constexpr int NYW = cdiv(YITEMS, 64), XL0 = 64 * NYW, BL0 = rup64(XL0 + UX), NAW = cdiv(UA, 64);
+    static_assert(BL0 + UB <= NT && NAW <= 4 && (NYW == 5 || NYW == 6) && BPOS == 32 && TX == 32 &&
+                      NIN <= 2 * NT && TY <= TY_MAX,
                   "lanes");
     // every segment starts on a 16-byte boundary (rows are read as float4)
     static_assert(XR >= AX && ASEG * SA == (ASWAP ? TY : TX) && BSEG * SB == (ASWAP ? TX : TY) && SX % 4 == 0 && SY % 4 == 0 &&
@@ -103,7 +103,7 @@ struct Geo {
     // A segment reads row_read(S + 2H) floats from its start; reads past a row's end stay inside
     // the buffer (the next row or the spare floats) and only feed outputs that are never used.
     static_assert(SX + row_read(SX + 2 * H) <= ZS + PAD && YR - SY + row_read(SY + 2 * H) <= XS + PAD &&
-                      (ASEG - 1) * SA + row_read(SX + 2 * H) <= GS + PAD && (BSEG - 1) * SB + row_read(SB + 2 * H) <= GXS + PAD,
+                      (ASEG - 1) * SA + row_read(SA + 2 * H) <= GS + PAD && (BSEG - 1) * SB + row_read(SB + 2 * H) <= GXS + PAD,
                   "row reads");
     static constexpr int LDS_FLOATS = 5 * (ZP + XP) + 3 * (GP + GXP + GYP) + 4 * PAD;
     static_assert(LDS_FLOATS * 4 <= 160 * 1024, "LDS");
@@ -142,30 +142,49 @@ FL_HD inline bool f_column(int c, int& ix, int& iy, int& zaddr) {
     return true;
 }
 
-// P1 unit of lane u: 1 = X (x-sums of one z-sum over one segment of row iy: reads Zs from src,
-// writes Xs at dst + i * XS), 2 = AX (x-sums of one adjoint field over one segment of row ay:
-// reads Gs from src, writes GXs at dst + i * GXS), 0 = none.
-template <class G, bool ADJ>
-FL_HD inline int p1_unit(int u, int& src, int& dst) {
+// X unit of lane tid (phase P1): x-sums of one z-sum over one segment of row iy; reads Zs from
+// src, writes Xs at dst + i * XS. Returns false for lanes without a unit.
+template <class G>
+FL_HD inline bool x_unit(int tid, int& src, int& dst) {
     src = 0;
     dst = 0;
-    if (u < G::UX) {
-        int row, iy;  // rows (q, seg) of IY positions
-        split32<G::IY>(u, 5 * G::XSEG, row, iy);
-        const int q = row / G::XSEG, start = (row % G::XSEG) * G::SX;
-        src = q * G::ZP + iy * G::ZS + start;
-        dst = q * G::XP + start * G::XS + iy;
-        return 1;
-    }
-    if (ADJ && u >= G::AX_LANE0 && u < G::AX_LANE0 + G::UA) {
-        int row, pos;  // rows (c, seg) of APOS positions
-        split32<G::APOS>(u - G::AX_LANE0, G::NADJ * G::ASEG, row, pos);
-        const int c = row / G::ASEG, start = (row % G::ASEG) * G::SA;
-        src = c * G::GP + pos * G::GS + start;
-        dst = c * G::GXP + start * G::GXS + pos;
-        return 2;
-    }
-    return 0;
+    const int u = tid - G::XL0;
+    if (u < 0 || u >= G::UX) return false;
+    int row, iy;  // rows (q, seg) of IY positions
+    split32<G::IY>(u, 5 * G::XSEG, row, iy);
+    const int q = row / G::XSEG, start = (row % G::XSEG) * G::SX;
+    src = q * G::ZP + iy * G::ZS + start;
+    dst = q * G::XP + start * G::XS + iy;
+    return true;
+}
+
+// The waves of the AX units: those of the SIMDs with fewer Y waves first (6 Y waves: SIMDs 0
+// and 1 carry two each; 5: SIMD 0 does).
+template <class G>
+FL_HD constexpr int ax_wave(int slot) {
+    return G::NYW == 6 ? (slot == 0 ? 6 : slot == 1 ? 7 : slot == 2 ? 10 : 11)
+                       : (slot == 0 ? 5 : slot == 1 ? 6 : slot == 2 ? 7 : 9);
+}
+
+// AX unit of lane tid (phase P0): sums of one adjoint field over one segment of position pos
+// (x-sums of adjoint row pos, or y-sums of adjoint column pos with ASWAP); reads Gs from src,
+// writes GXs at dst + i * GXS. Returns false for lanes without a unit.
+template <class G>
+FL_HD inline bool ax_unit(int tid, int& src, int& dst) {
+    src = 0;
+    dst = 0;
+    const int wave = tid >> 6;
+    int slot = -1;
+    for (int s = 0; s < G::NAW; ++s)
+        if (ax_wave<G>(s) == wave) slot = s;
+    const int u = slot * 64 + (tid & 63);
+    if (slot < 0 || u >= G::UA) return false;
+    int row, pos;  // rows (c, seg) of APOS positions
+    split32<G::APOS>(u, G::NADJ * G::ASEG, row, pos);
+    const int c = row / G::ASEG, start = (row % G::ASEG) * G::SA;
+    src = c * G::GP + pos * G::GS + start;
+    dst = c * G::GXP + start * G::GXS + pos;
+    return true;
 }
 
 // Y item of lane tid < YITEMS: adjoint column ax and segment seg (rows y_start = seg * SY ...).
@@ -179,20 +198,16 @@ FL_HD inline int y_gs(int c, int ax, int ay) {
     return c * G::GP + (G::ASWAP ? ax * G::GS + ay : ay * G::GS + ax);
 }
 
-// AYs unit of lane tid, on waves 10, 11, 14, 15, B_PER_WAVE lanes each: sums of one adjoint field
-// over one segment of position pos (y-sums of output column pos, or x-sums of output row pos with
-// ASWAP); reads GXs from src, writes GY at dst + i * BW. Returns false for lanes without a unit.
+// AYs unit of lane tid (phase P1): sums of one adjoint field over one segment of position pos
+// (y-sums of output column pos, or x-sums of output row pos with ASWAP); reads GXs from src,
+// writes GY at dst + i * BW. Returns false for lanes without a unit.
 template <class G>
 FL_HD inline bool ays_unit(int tid, int& src, int& dst) {
     src = 0;
     dst = 0;
-    const int wave = tid >> 6, l = tid & 63;
-    const int bslot = wave == 10 ? 0 : wave == 11 ? 1 : wave == 14 ? 2 : wave == 15 ? 3 : -1;
-    if (bslot < 0 || l >= G::B_PER_WAVE) return false;
-    // rows (c, seg) of BPOS = 32 positions: slot s takes row s on its first 32 lanes and half of
-    // row 4 + s/2 on the next 16
-    const int row = l < 32 ? bslot : 4 + (bslot >> 1);
-    const int pos = l < 32 ? l : (bslot & 1) * 16 + (l - 32);
+    const int u = tid - G::BL0;
+    if (u < 0 || u >= G::UB) return false;
+    const int row = u >> 5, pos = u & 31;  // rows (c, seg) of BPOS = 32 positions
     const int c = row / G::BSEG, start = (row % G::BSEG) * G::SB;
     src = c * G::GXP + pos * G::GXS + start;
     dst = c * G::GYP + (G::ASWAP ? pos * G::GYS + start : start * G::GYS + pos);

@@ -53,9 +53,17 @@ FL_UNROLL
 // over the K planes ending at this one. The march is unrolled by K and R = the step's position in
 // its block of K planes = the ring slot of this plane. pre holds the sums over the current block
 // (slots 0..R after this step), the ring p, t of the last K planes: slots 0..R this block's,
-// slots R+1..K-1 the previous block's, which complete the window. The ring starts at zero.
-template <int K, int R>
-FL_WHD inline void zstep5(float p, float t, float (&pre)[5], float (&pr)[K], float (&tr)[K], float (&out)[5]) {
+// slots R+1..K-1 the previous block's, which complete the window. With M > 0 the previous block's
+// sums over slots M..K-1 are kept as one partial sum per field (ch), formed from the ring when a
+// block completes (R = K-1): a step R < M adds the ring's slots R+1..M-1 and ch, a step R >= M adds
+// slots R+1..K-1. Each window is still a sum of its own K terms (in another order), and a step costs
+// M(M+1)/2 + (K-1-M)(K-M)/2 + (K-1-M) adds per block and field instead of K(K-1)/2 (M = 0 or
+// K-1: no chain). The ring and ch start at zero.
+template <int K, int R, int M = 0>
+FL_WHD inline void zstep5(float p, float t, float (&pre)[5], float (&pr)[K], float (&tr)[K], float (&ch)[5],
+                          float (&out)[5]) {
+    static_assert(M >= 0 && M < K, "chain split");
+    constexpr bool CH = M > 0 && M < K - 1;
     if constexpr (R == 0) {
         pre[0] = p;
         pre[1] = t;
@@ -71,31 +79,63 @@ FL_WHD inline void zstep5(float p, float t, float (&pre)[5], float (&pr)[K], flo
     }
 FL_UNROLL
     for (int q = 0; q < 5; ++q) out[q] = pre[q];
+    constexpr int E = (CH && R < M) ? M : K;   // ring slots R+1..E-1 are added from the ring
 FL_UNROLL
-    for (int s = R + 1; s < K; ++s) {
+    for (int s = R + 1; s < E; ++s) {
         out[0] += pr[s];
         out[1] += tr[s];
         out[2] = __builtin_fmaf(pr[s], pr[s], out[2]);
         out[3] = __builtin_fmaf(tr[s], tr[s], out[3]);
         out[4] = __builtin_fmaf(pr[s], tr[s], out[4]);
     }
+    if constexpr (CH && R < M) {
+FL_UNROLL
+        for (int q = 0; q < 5; ++q) out[q] += ch[q];
+    }
     pr[R] = p;
     tr[R] = t;
+    if constexpr (CH && R == K - 1) {
+        // the block is complete: its sums over slots M..K-1, from the last slot down
+        ch[0] = pr[K - 1];
+        ch[1] = tr[K - 1];
+        ch[2] = pr[K - 1] * pr[K - 1];
+        ch[3] = tr[K - 1] * tr[K - 1];
+        ch[4] = pr[K - 1] * tr[K - 1];
+FL_UNROLL
+        for (int s = K - 2; s >= M; --s) {
+            ch[0] += pr[s];
+            ch[1] += tr[s];
+            ch[2] = __builtin_fmaf(pr[s], pr[s], ch[2]);
+            ch[3] = __builtin_fmaf(tr[s], tr[s], ch[3]);
+            ch[4] = __builtin_fmaf(pr[s], tr[s], ch[4]);
+        }
+    }
 }
 
 // The same for one field y (the xy-sums of an adjoint coefficient): returns the sum over the K
-// planes ending at this one.
-template <int K, int R>
+// planes ending at this one. With the chain (M as above) the previous block's sum over slots
+// M..K-1 is formed in ring slot M itself when a block completes (that slot's own value is not read
+// again before the next block overwrites it), so the chain costs no register.
+template <int K, int R, int M = 0>
 FL_WHD inline float zstep1(float y, float& pre, float (&ring)[K]) {
+    static_assert(M >= 0 && M < K, "chain split");
+    constexpr bool CH = M > 0 && M < K - 1;
     if constexpr (R == 0) {
         pre = y;
     } else {
         pre += y;
     }
     float out = pre;
+    constexpr int E = (CH && R < M) ? M + 1 : K;   // slots R+1..E-1 (slot M = the chain when R < M)
 FL_UNROLL
-    for (int s = R + 1; s < K; ++s) out += ring[s];
+    for (int s = R + 1; s < E; ++s) out += ring[s];
     ring[R] = y;
+    if constexpr (CH && R == K - 1) {
+        float c = ring[K - 1];
+FL_UNROLL
+        for (int s = K - 2; s > M; --s) c += ring[s];
+        ring[M] += c;
+    }
     return out;
 }
 

@@ -80,7 +80,7 @@ long check(int plant) {
         for (int a = 0; a < NARR; ++a) m.writes[p][a].assign(m.size[a], 0);
     }
     const int rows_x = fl::row_read(G::SX + 2 * H);                       // X row read (floats)
-    const int rows_a = fl::row_read(G::SX + 2 * H);  // AX row read: the unit row is read as an X row
+    const int rows_a = fl::row_read(G::SA + 2 * H);                       // AX row read
     const int rows_y = fl::row_read(G::SY + 2 * H) - (plant == 2 ? 1 : 0);
     const int rows_b = fl::row_read(G::SB + 2 * H);
 
@@ -100,24 +100,28 @@ long check(int plant) {
             if (plant == 1) zaddr += 1;
             for (int q = 0; q < 5; ++q) m.write(0, ZS, (long)q * G::ZP + zaddr);
         }
-        // P0 / Y: the NA adjoint fields of SY outputs of column ax
+        // P1 / Y: the NA adjoint fields of SY outputs of column ax
         if (tid < G::YITEMS) {
             int seg, ax;
             fl::y_item<G>(tid, seg, ax);
             for (int c = 0; c < NA; ++c)
-                for (int i = 0; i < G::SY; ++i) m.write(0, GS, fl::y_gs<G>(c, ax, seg * G::SY + i));
+                for (int i = 0; i < G::SY; ++i) m.write(1, GS, fl::y_gs<G>(c, ax, seg * G::SY + i));
         }
-        // P0 / AYs
+        // P1 / AYs
         int bsrc, bdst;
         if (fl::ays_unit<G>(tid, bsrc, bdst))
-            for (int i = 0; i < G::SB; ++i) m.write(0, GY, bdst + (long)i * (G::BW - (plant == 3 ? 1 : 0)));
-        // P1 / X and AX
+            for (int i = 0; i < G::SB; ++i) m.write(1, GY, bdst + (long)i * (G::BW - (plant == 3 ? 1 : 0)));
+        // P1 / X, P0 / AX
         int src, dst;
-        const int kind = fl::p1_unit<G, true>(tid, src, dst);
-        if (kind == 1)
+        if (fl::x_unit<G>(tid, src, dst))
             for (int i = 0; i < G::SX; ++i) m.write(1, XS, dst + (long)i * G::XS);
-        if (kind == 2)
-            for (int i = 0; i < G::SA; ++i) m.write(1, GXS, dst + (long)i * G::GXS);
+        if (fl::ax_unit<G>(tid, src, dst))
+            for (int i = 0; i < G::SA; ++i) m.write(0, GXS, dst + (long)i * G::GXS);
+        // lane kinds: a lane has at most one of Y, X, AYs (P1) and at most one of Y, AX (P0)
+        int s2, d2;
+        const int p1 = (tid < G::YITEMS) + fl::x_unit<G>(tid, s2, d2) + fl::ays_unit<G>(tid, s2, d2);
+        const int p0 = (tid < G::YITEMS) + fl::ax_unit<G>(tid, s2, d2);
+        if (p1 > 1 || p0 > 1) m.fail("lane " + std::to_string(tid) + " has two units in one phase");
     }
     // ---- races: one write per address per phase
     for (int p = 0; p < 2; ++p)
@@ -147,19 +151,18 @@ long check(int plant) {
                 }
             }
         }
-        // P0 / AYs reads rows of GXs; every output oy < TY is used
+        // P1 / AYs reads rows of GXs; every output oy < TY is used
         int bsrc, bdst;
         if (fl::ays_unit<G>(tid, bsrc, bdst)) {
-            m.read(0, GXS, bsrc, rows_b);
+            m.read(1, GXS, bsrc, rows_b);
             for (int i = 0; i < G::SB; ++i) {
-                m.used(0, GXS, bsrc + i, 2 * H + 1);
+                m.used(1, GXS, bsrc + i, 2 * H + 1);
                 ++used_outputs;
             }
         }
-        // P1 / X reads rows of Zs (outputs ax < AX used), AX reads rows of Gs (all used)
+        // P1 / X reads rows of Zs (outputs ax < AX used), P0 / AX reads rows of Gs (all used)
         int src, dst;
-        const int kind = fl::p1_unit<G, true>(tid, src, dst);
-        if (kind == 1) {
+        if (fl::x_unit<G>(tid, src, dst)) {
             const long s = src + (plant == 4 ? 5L * G::ZP : 0);
             m.read(1, ZS, s, rows_x);
             const int start = (dst % G::XP) / G::XS;  // first output position of the segment
@@ -169,22 +172,22 @@ long check(int plant) {
                 ++used_outputs;
             }
         }
-        if (kind == 2) {
-            m.read(1, GS, src, rows_a);
+        if (fl::ax_unit<G>(tid, src, dst)) {
+            m.read(0, GS, src, rows_a);
             for (int i = 0; i < G::SA; ++i) {
                 if (i + 2 * H + 1 > rows_a) m.fail("AX window past the row read");
-                m.used(1, GS, src + i, 2 * H + 1);
+                m.used(0, GS, src + i, 2 * H + 1);
                 ++used_outputs;
             }
         }
-        // P1 / AZ reads one xy-sum per field of its output column
+        // P0 / AZ reads one xy-sum per field of its output column
         if (tid < G::NOUT) {
             int ox, oy;
             fl::az_lane<G>(tid, ox, oy);
             for (int c = 0; c < NA; ++c) {
                 const long a = (long)c * G::GYP + oy * G::GYS + ox;
-                m.read(1, GY, a, 1);
-                m.used(1, GY, a, 1);
+                m.read(0, GY, a, 1);
+                m.used(0, GY, a, 1);
                 ++used_outputs;
             }
         }

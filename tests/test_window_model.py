@@ -1,9 +1,10 @@
 """The window sums of the fused kernel (fused-lncc_amd/csrc/lncc_window.h), checked on the host by
 tests/window_model.cpp: exact on integer data, exactly zero on zero windows and exactly K*c on
 windows of one constant inside random data, within the direct-sum error bound everywhere, for the
-x/y segment lengths and the D-march (with zero and constant slabs after signal) of every k. These
-are the properties of the reference's direct k-tap sums (fused_lncc/csrc/lncc3d.cu:57-92) that the
-kernel's sums must share. Planted mistakes (running sums along D, a dropped term) must be reported."""
+x/y segment lengths and the D-march (with zero and constant slabs after signal) of every k, with
+each split of the previous block's suffix kept as a partial sum. These are the properties of the
+reference's direct k-tap sums (fused_lncc/csrc/lncc3d.cu:57-92) that the kernel's sums must share.
+Planted mistakes (running sums along D, a dropped term, a damaged suffix chain) must be reported."""
 import os
 import shutil
 import subprocess
@@ -32,10 +33,12 @@ def test_window_sums_are_window_local(model):
     assert r.returncode == 0, r.stdout + r.stderr
     lines = r.stdout.strip().splitlines()
     assert lines[-1] == "all ok"
-    assert len([ln for ln in lines if ln.endswith(": ok")]) == 17
+    # 13 segment checks, and the march for every k = 3..9 and every chain split M = 0..k-1
+    assert len([ln for ln in lines if ln.endswith(": ok")]) == 13 + 3 + 5 + 7 + 9
 
 
-@pytest.mark.parametrize("plant,what", [(1, "march K=7: FAILED"), (2, "box_sums h=3 S=20 (x): FAILED")])
+@pytest.mark.parametrize("plant,what", [(1, "march K=7 chain M=0: FAILED"), (2, "box_sums h=3 S=20 (x): FAILED"),
+                                        (3, "march K=7 chain M=4: FAILED")])
 def test_planted_mistakes_are_reported(model, plant, what):
     r = subprocess.run([model, str(plant)], capture_output=True, text=True)
     assert r.returncode == 1 and what in r.stdout, r.stdout

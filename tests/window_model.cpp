@@ -10,11 +10,13 @@
 //            0.1f, every order of summation rounds differently and only the bound applies);
 //   bound    on random data every window is within (K-1) * 2^-24 * sum|v| of the float64 sum,
 //            the error bound of a direct sum of K terms.
-// The march is run over 300 planes with zero and constant slabs after signal, for K = 3..9.
+// The march is run over 300 planes with zero and constant slabs after signal, for K = 3..9 and
+// every split M of the previous block's suffix (the chain of zstep5 / zstep1; M = 0: none).
 //
 // Usage: window_model [plant]. plant = 1 replaces zstep5's window by a running sum (add the
 // entering plane, subtract the leaving one), plant = 2 drops the last term of box_sums' block
-// suffix; each must be reported. Prints one line per check group and exits 0 when all pass.
+// suffix, plant = 3 halves zstep5's chain of the previous block's suffix (for every split M > 0);
+// each must be reported. Prints one line per check group and exits 0 when all pass.
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -87,8 +89,8 @@ void check_box(std::mt19937& rng, const char* name) {
     std::printf("box_sums h=%d S=%d (%s): %s\n", H, S, name, g_fail == before ? "ok" : "FAILED");
 }
 
-template <int K, int R>
-void step5(float p, float t, float (&pre)[5], float (&pr)[K], float (&tr)[K], float (&out)[5]) {
+template <int K, int R, int M>
+void step5(float p, float t, float (&pre)[5], float (&pr)[K], float (&tr)[K], float (&ch)[5], float (&out)[5]) {
     if (g_plant == 1) {
         // model of the bug this replaces: running sums over the whole march
         static float acc[5];
@@ -102,26 +104,29 @@ void step5(float p, float t, float (&pre)[5], float (&pr)[K], float (&tr)[K], fl
         pr[R] = p;
         tr[R] = t;
         (void)pre;
+        (void)ch;
         return;
     }
-    fl::zstep5<K, R>(p, t, pre, pr, tr, out);
+    fl::zstep5<K, R, M>(p, t, pre, pr, tr, ch, out);
+    if (g_plant == 3 && R == K - 1) ch[0] *= 0.5f;  // a chain that loses half of its p terms
 }
 
-template <int K, int R = 0>
-void march_step(int r, float p, float t, float (&pre)[5], float (&pr)[K], float (&tr)[K], float (&out)[5],
-                float y, float& gpre, float (&gr)[K], float& gout) {
+template <int K, int M, int R = 0>
+void march_step(int r, float p, float t, float (&pre)[5], float (&pr)[K], float (&tr)[K], float (&ch)[5],
+                float (&out)[5], float y, float& gpre, float (&gr)[K], float& gout) {
     if constexpr (R < K) {
         if (r == R) {
-            step5<K, R>(p, t, pre, pr, tr, out);
-            gout = fl::zstep1<K, R>(y, gpre, gr);
+            step5<K, R, M>(p, t, pre, pr, tr, ch, out);
+            gout = fl::zstep1<K, R, M>(y, gpre, gr);
         } else {
-            march_step<K, R + 1>(r, p, t, pre, pr, tr, out, y, gpre, gr, gout);
+            march_step<K, M, R + 1>(r, p, t, pre, pr, tr, ch, out, y, gpre, gr, gout);
         }
     }
 }
 
-// the D-march: one column over 300 planes, signal then zero then constant slabs
-template <int K>
+// the D-march: one column over 300 planes, signal then zero then constant slabs; M = the split
+// of the previous block's suffix (0 = none)
+template <int K, int M>
 void check_march(std::mt19937& rng) {
     const int Z = 300;
     const long before = g_fail;
@@ -135,9 +140,9 @@ void check_march(std::mt19937& rng) {
             if (kind >= 1 && z >= 100 && z < 180) p[z] = t[z] = y[z] = 0.f;         // zero slab
             if (kind >= 1 && z >= 220 && z < 280) p[z] = t[z] = y[z] = (kind == 1 ? 128.f : 0.5f);  // constant slab
         }
-        float pre[5] = {0}, pr[K] = {0}, tr[K] = {0}, out[5], gpre = 0.f, gr[K] = {0}, gout;
+        float pre[5] = {0}, pr[K] = {0}, tr[K] = {0}, ch[5] = {0}, out[5], gpre = 0.f, gr[K] = {0}, gout;
         for (int z = 0; z < Z; ++z) {
-            march_step<K>(z % K, p[z], t[z], pre, pr, tr, out, y[z], gpre, gr, gout);
+            march_step<K, M>(z % K, p[z], t[z], pre, pr, tr, ch, out, y[z], gpre, gr, gout);
             // direct sums of the window [z-K+1, z] (planes before 0 are zero)
             double ref[5] = {0}, mag[5] = {0}, gref = 0.0, gmag = 0.0;
             float r32[5] = {0}, g32 = 0.f;
@@ -177,7 +182,16 @@ void check_march(std::mt19937& rng) {
                 fail("march K=" + std::to_string(K) + ": adjoint window beyond the bound");
         }
     }
-    std::printf("march K=%d: %s\n", K, g_fail == before ? "ok" : "FAILED");
+    std::printf("march K=%d chain M=%d: %s\n", K, M, g_fail == before ? "ok" : "FAILED");
+}
+
+// every split of the previous block's suffix, M = 0 (none) .. K-1
+template <int K, int M = 0>
+void check_all_splits(std::mt19937& rng) {
+    if constexpr (M < K) {
+        check_march<K, M>(rng);
+        check_all_splits<K, M + 1>(rng);
+    }
 }
 
 }  // namespace
@@ -199,10 +213,10 @@ int main(int argc, char** argv) {
     check_box<3, 16>(rng, "ax/ays");
     check_box<4, 16>(rng, "ax");
     check_box<4, 12>(rng, "ays");
-    check_march<3>(rng);
-    check_march<5>(rng);
-    check_march<7>(rng);
-    check_march<9>(rng);
+    check_all_splits<3>(rng);
+    check_all_splits<5>(rng);
+    check_all_splits<7>(rng);
+    check_all_splits<9>(rng);
     std::printf("%s\n", g_fail ? "FAILED" : "all ok");
     return g_fail ? 1 : 0;
 }
