@@ -48,7 +48,7 @@ int device_cus() {
 }
 
 // Workgroups: B volumes x (W/TX) x (H/TY) tiles x D-chunks. A chunk of d output planes costs
-// d + 4h + 2 pipeline steps (it recomputes the halo planes of its neighbours), so D is split only
+// d + 4h + 3 pipeline steps (it recomputes the halo planes of its neighbours), so D is split only
 // where that shortens the launch: small volumes, whose tiles alone leave CUs idle, get short chunks.
 // fl_test_set_dchunk fixes the chunk length for the calling thread (tests of chunk seams and of
 // long unsplit marches).
@@ -58,7 +58,7 @@ Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     p.ntx = (int)((W + fl::TX - 1) / fl::TX);
     p.nty = (int)((H + ty - 1) / ty);
     const int64_t base = B * p.ntx * p.nty;
-    // Split D into nzc chunks. A chunk of d planes costs d + 4h + 2 pipeline steps, and the
+    // Split D into nzc chunks. A chunk of d planes costs d + 4h + 3 pipeline steps, and the
     // workgroups run in rounds of one per CU: pick the split with the fewest rounds x steps (ties:
     // fewer workgroups).
     const int64_t kCUs = device_cus();
@@ -66,7 +66,7 @@ Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     for (int64_t nzc = 1; nzc <= D; ++nzc) {
         const int64_t d = (D + nzc - 1) / nzc;
         const int64_t blocks = base * ((D + d - 1) / d);
-        const int64_t cost = ((blocks + kCUs - 1) / kCUs) * (d + 4 * halo + 2);
+        const int64_t cost = ((blocks + kCUs - 1) / kCUs) * (d + 4 * halo + 3);
         if (best_cost < 0 || cost < best_cost) {
             best_cost = cost;
             dchunk = d;

@@ -247,7 +247,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // z-window chains (zstep5 / zstep1): the previous block's sums over ring slots F_CHAIN..K-1
     // (F) and A_CHAIN..K-1 (AZ) kept as partial sums; 0 = none
     constexpr int F_CHAIN = HH == 3 ? 4 : 0;
-    constexpr int A_CHAIN = HH >= 2 && HH <= 3 ? HH + 1 : 0;
+    constexpr int A_CHAIN = HH >= 2 && (HH <= 3 || !BF16) ? HH + 1 : 0;
 
     // Stage bodies; the march below orders them per phase.
     //
