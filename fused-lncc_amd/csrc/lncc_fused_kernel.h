@@ -93,6 +93,17 @@ __device__ __forceinline__ void lds_row(const float* __restrict__ src, float (&v
     }
 }
 
+// Stores four floats to a 16-byte aligned LDS address as one 128-bit write. The vector passes
+// through an empty asm operand that needs all of its lanes, for the reason given at lds_row: left
+// alone, the compiler split the AYs stores into pairs of adjacent 32-bit writes (ds_write2_b32),
+// and at the row stride of GY (36 floats) each such write served 64 lanes from 16 banks, 4-way
+// conflicts: a quarter of the kernel's LDS bank-conflict cycles came from them.
+__device__ __forceinline__ void lds_store4(float* __restrict__ dst, float x, float y, float z, float w) {
+    lds_f4 f = {x, y, z, w};
+    asm("" : "+v"(f));
+    *reinterpret_cast<lds_f4*>(dst) = f;
+}
+
 template <int HH, bool BF16, int MODE>
 __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) {
     constexpr bool ADJ = (MODE == MODE_GRAD);
@@ -307,7 +318,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             static_assert(G::SY == 4, "float4 rows");
 #pragma unroll
             for (int c = 0; c < 3; ++c)
-                *reinterpret_cast<lds_f4*>(Gs + y_gs<G>(c, y_ax, y_start)) = lds_f4{adj[c][0], adj[c][1], adj[c][2], adj[c][3]};
+                lds_store4(Gs + y_gs<G>(c, y_ax, y_start), adj[c][0], adj[c][1], adj[c][2], adj[c][3]);
         }
         loss_acc += (double)lsum;
     };
@@ -487,7 +498,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 for (int i = 0; i < G::SB; ++i) {
                     if constexpr (G::ASWAP) {  // GY rows along x: float4s
                         if (i % 4 == 0)
-                            *reinterpret_cast<lds_f4*>(GY + u_dst + i) = lds_f4{o[i], o[i + 1], o[i + 2], o[i + 3]};
+                            lds_store4(GY + u_dst + i, o[i], o[i + 1], o[i + 2], o[i + 3]);
                     } else {
                         GY[u_dst + i * G::BW] = o[i];
                     }
