@@ -176,7 +176,20 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     }
     const bool has_y = tid < G::YITEMS;
     int y_seg = 0, y_ax = 0;  // rows seg of AX positions
-    if (has_y) y_item<G>(tid, y_seg, y_ax);
+    // the Y item's offsets into Xs and Gs. At k = 7 they take the registers of the X / AYs unit
+    // offsets (a Y lane has no such unit), which with three of Y's rows in flight across F is
+    // what keeps the kernel within 128 registers; at the other k separate registers measured
+    // faster (k = 9: 1%).
+    constexpr bool Y_SHARE = HH == 3;
+    int y_xs = 0, y_gs0 = 0;
+    if (has_y) {
+        y_item<G>(tid, y_seg, y_ax);
+        if constexpr (Y_SHARE)
+            y_offsets<G>(tid, u_src, u_dst);
+        else
+            y_offsets<G>(tid, y_xs, y_gs0);
+    }
+    const int y_xo = Y_SHARE ? u_src : y_xs, y_go = Y_SHARE ? u_dst : y_gs0;
     const int y_start = y_seg * G::SY;
     // per output of the Y segment: inside the volume (ncc and adjoints live) / counted in the loss
     // (inside the volume and in the output tile); the same on every plane
@@ -256,8 +269,11 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const int zn_hi = min(zhi, D);                 // F: new plane zi+1 valid while zi+1 < zn_hi
     constexpr int ZO = 3 + 2 * HH;                 // AZ: output plane zi-ZO
     // z-window chains (zstep5 / zstep1): the previous block's sums over ring slots F_CHAIN..K-1
-    // (F) and A_CHAIN..K-1 (AZ) kept as partial sums; 0 = none
-    constexpr int F_CHAIN = HH == 3 ? 4 : 0;
+    // (F) and A_CHAIN..K-1 (AZ) kept as partial sums; 0 = none. F's chain (slots 4..6 at k = 7)
+    // saves adds but holds five more registers per column; at k = 7 those registers measured
+    // better spent on Y's rows in flight across F (three rows and no chain: 2.7% faster than one
+    // row and the chain), and at k = 9 they are not there.
+    constexpr int F_CHAIN = 0;
     constexpr int A_CHAIN = HH >= 2 && (HH <= 3 || !BF16) ? HH + 1 : 0;
 
     // Stage bodies; the march below orders them per phase.
@@ -294,9 +310,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     adj[1][i] = crm * uu;
                     adj[2][i] = crm;
                 } else {
-                    Gs[y_gs<G>(0, y_ax, ay)] = crm * w;
-                    Gs[y_gs<G>(1, y_ax, ay)] = crm * uu;
-                    Gs[y_gs<G>(2, y_ax, ay)] = crm;
+                    Gs[y_go + i * G::GST] = crm * w;
+                    Gs[y_go + G::GP + i * G::GST] = crm * uu;
+                    Gs[y_go + 2 * G::GP + i * G::GST] = crm;
                 }
             }
             if constexpr (MODE == MODE_MAPS) {
@@ -318,7 +334,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             static_assert(G::SY == 4, "float4 rows");
 #pragma unroll
             for (int c = 0; c < 3; ++c)
-                lds_store4(Gs + y_gs<G>(c, y_ax, y_start), adj[c][0], adj[c][1], adj[c][2], adj[c][3]);
+                lds_store4(Gs + y_go + c * G::GP, adj[c][0], adj[c][1], adj[c][2], adj[c][3]);
         }
         loss_acc += (double)lsum;
     };
@@ -363,8 +379,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // Stage order inside a phase. Each wave runs its stages in program order, so a stage placed
     // between the issue of another stage's LDS reads and their use hides part of their latency.
     //  * P0: AZ's xy-sums are read first. The Y lanes read Y_EARLY of their five rows (all five
-    //    at k <= 5, one at k = 7: more rows held across F exceed the 128-register budget of a
-    //    1024-lane workgroup) and at k <= 5 the AX lanes their row, F runs while they arrive, then
+    //    at k <= 5, three at k = 7, two for bf16 at k = 7: more rows held across F exceed the
+    //    128-register budget of a 1024-lane workgroup) and at k <= 5 the AX lanes their row, F
+    //    runs while they arrive, then
     //    the Y lanes read their other rows and form the five box sums, which stay in registers
     //    until P1, and the AX lanes their sums; AZ's z-sums and the gradient come last. At k = 9
     //    (two rings of 9 planes) nothing is read early and Y's rows are read one at a time. (At
@@ -372,7 +389,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     //  * P1: the Y lanes turn their box sums into ncc and the adjoint coefficients (arithmetic
     //    only, no LDS reads: it keeps the SIMDs busy while the rows of the X and AYs units, on the
     //    other waves, arrive), then the X and AYs units.
-    constexpr int Y_EARLY = HH <= 2 ? 5 : HH == 3 ? 1 : 0;   // Y rows read before F
+    constexpr int Y_EARLY = HH <= 2 ? 5 : HH == 3 ? (BF16 ? 2 : 3) : 0;   // Y rows read before F
     constexpr bool F_STORE_AT_ONCE = Y_EARLY < 5;
     constexpr bool AX_EARLY = HH <= 2;                        // the AX row read before F
     constexpr int NY = G::SY + 2 * HH, NA = G::SA + 2 * HH, NX = G::SX + 2 * HH, NB = G::SB + 2 * HH;
@@ -412,7 +429,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 #pragma unroll
                 for (int q = 0; q < Y_EARLY; ++q) {
                     float v[NY];
-                    lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, v);
+                    lds_row(Xs + q * G::XP + y_xo, v);
 #pragma unroll
                     for (int i = 0; i < NY; ++i) er[q * NY + i] = v[i];
                 }
@@ -432,7 +449,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 #pragma unroll
                         for (int i = 0; i < NY; ++i) v[i] = er[(q < Y_EARLY ? q : 0) * NY + i];
                     } else {
-                        lds_row(Xs + q * G::XP + y_ax * G::XS + y_start, v);
+                        lds_row(Xs + q * G::XP + y_xo, v);
                     }
                     box_sums<HH, G::SY>(v, S[q]);
                 }

@@ -90,6 +90,7 @@ struct Geo {
     // Gs rows along x (along y with ASWAP), GXs rows along y (x), GY rows along x
     static constexpr int GS = ASWAP ? stride4(YR) : stride4(AX), GXS = ASWAP ? stride4(AX) : XS;
     static constexpr int GYS = ASWAP ? stride4(TX) : TX + 1, BW = ASWAP ? 1 : GYS, PAD = 16;
+    static constexpr int GST = ASWAP ? 1 : GS;  // stride of a Y item's consecutive outputs in Gs
     // The planes F writes (one column, five fields) and AZ reads (one column, three fields) are a
     // multiple of 64 floats apart for k >= 5, so that those accesses pair into write2st64 /
     // read2st64 (6 LDS instructions per lane and step instead of 10 for F, 5 with FPAIR; 2 instead
@@ -196,6 +197,15 @@ FL_HD inline void y_item(int tid, int& seg, int& ax) {
 template <class G>
 FL_HD inline int y_gs(int c, int ax, int ay) {
     return c * G::GP + (G::ASWAP ? ax * G::GS + ay : ay * G::GS + ax);
+}
+// The same as two offsets per lane: the item's rows start at xs in every Xs plane (q * XP + xs),
+// and output i of adjoint field c goes to Gs at gs + c * GP + i * GST (= y_gs(c, ax, seg*SY + i)).
+template <class G>
+FL_HD inline void y_offsets(int tid, int& xs, int& gs) {
+    int seg, ax;
+    y_item<G>(tid, seg, ax);
+    xs = ax * G::XS + seg * G::SY;
+    gs = y_gs<G>(0, ax, seg * G::SY);
 }
 
 // AYs unit of lane tid (phase P1): sums of one adjoint field over one segment of position pos

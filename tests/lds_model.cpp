@@ -102,10 +102,15 @@ long check(int plant) {
         }
         // P1 / Y: the NA adjoint fields of SY outputs of column ax
         if (tid < G::YITEMS) {
-            int seg, ax;
+            int seg, ax, xs, gs;
             fl::y_item<G>(tid, seg, ax);
+            fl::y_offsets<G>(tid, xs, gs);  // the kernel's per-lane form of the same addresses
             for (int c = 0; c < NA; ++c)
-                for (int i = 0; i < G::SY; ++i) m.write(1, GS, fl::y_gs<G>(c, ax, seg * G::SY + i));
+                for (int i = 0; i < G::SY; ++i) {
+                    const int a = gs + c * G::GP + i * G::GST;
+                    if (a != fl::y_gs<G>(c, ax, seg * G::SY + i)) m.fail("Y offsets disagree with y_gs");
+                    m.write(1, GS, a);
+                }
         }
         // P1 / AYs
         int bsrc, bdst;
@@ -137,11 +142,13 @@ long check(int plant) {
     for (int tid = 0; tid < fl::NT; ++tid) {
         // P0 / Y reads rows of Xs; outputs ay < AY are used, each reading its 2h+1 window
         if (tid < G::YITEMS) {
-            int seg, ax;
+            int seg, ax, xs, gs;
             fl::y_item<G>(tid, seg, ax);
+            fl::y_offsets<G>(tid, xs, gs);
             const int y0 = seg * G::SY;
+            if (xs != ax * G::XS + y0) m.fail("Y row offset disagrees with the item");
             for (int q = 0; q < 5; ++q) {
-                const long row = (long)q * G::XP + (long)ax * G::XS + y0;
+                const long row = (long)q * G::XP + xs;
                 m.read(0, XS, row, rows_y);
                 for (int i = 0; i < G::SY; ++i) {
                     if (y0 + i >= G::AY || ax >= G::AX) continue;
