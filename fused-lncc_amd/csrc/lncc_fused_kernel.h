@@ -344,11 +344,12 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // (inactive ones through a zero-sized buffer), so the number of outstanding memory operations
     // is the same on every path and the waits before use stay exact. With STORE the z-sums go to
     // the LDS column by column as they are formed; without, f_store writes them later.
-    auto f_sums = [&](auto rc, auto store, int zi, uint64_t zoff) __attribute__((always_inline)) {
+    // F's columns [JB, JE) of this lane (f_sums runs them all, then the prefetch)
+    auto f_cols = [&](auto rc, auto store, auto jb, auto je) __attribute__((always_inline)) {
         constexpr int r = decltype(rc)::value;
         constexpr bool STORE = decltype(store)::value;
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
+        for (int j = decltype(jb)::value; j < decltype(je)::value; ++j) {
             zstep5<K, r, F_CHAIN>(pnext[j], tnext[j], fpre[j], pring[j], tring[j], fch[j], zsum[j]);
             if constexpr (STORE) {
                 if (G::FPAIR || zaddr[j] >= 0) {
@@ -357,6 +358,8 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 }
             }
         }
+    };
+    auto f_pref = [&](int zi, uint64_t zoff) __attribute__((always_inline)) {
         // prefetch plane zi+1
         const bool okn = zi + 1 < zn_hi;
         const __amdgpu_buffer_rsrc_t rpn = rsrc_at(pva + zoff + PB, plane_bytes, okn);
@@ -366,6 +369,10 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             pnext[j] = load_elem<BF16>(rpn, voff[j]);
             tnext[j] = load_elem<BF16>(rtn, voff[j]);
         }
+    };
+    auto f_sums = [&](auto rc, auto store, int zi, uint64_t zoff) __attribute__((always_inline)) {
+        f_cols(rc, store, std::integral_constant<int, 0>{}, std::integral_constant<int, J>{});
+        f_pref(zi, zoff);
     };
     auto f_store = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -391,6 +398,10 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     //    other waves, arrive), then the X and AYs units.
     constexpr int Y_EARLY = HH <= 2 ? 5 : HH == 3 ? (BF16 ? 2 : 3) : 0;   // Y rows read before F
     constexpr bool F_STORE_AT_ONCE = Y_EARLY < 5;
+    // k = 7 (fp32): the box sums of the early rows are formed between F's two columns, and the
+    // registers they free take Y_MID more rows, read before F's second column; the rest after F
+    constexpr int Y_MID = (HH == 3 && !BF16 && J == 2) ? 1 : 0;
+    static_assert(Y_EARLY + Y_MID <= 5, "Y rows");
     constexpr bool AX_EARLY = HH <= 2;                        // the AX row read before F
     constexpr int NY = G::SY + 2 * HH, NA = G::SA + 2 * HH, NX = G::SX + 2 * HH, NB = G::SB + 2 * HH;
     // P0's early reads (Y's first rows or the AX row) share one register array: the two kinds of
@@ -439,9 +450,47 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 #pragma unroll
                 for (int i = 0; i < NA; ++i) er[i] = v[i];
             }
-            f_sums(rc, std::integral_constant<bool, F_STORE_AT_ONCE>{}, zi, zoff);
             float S[5][G::SY];  // Y's box sums, carried into P1
-            if (has_y && actY) {
+            if constexpr (Y_MID > 0) {
+                f_cols(rc, std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+                float em[Y_MID > 0 ? Y_MID * NY : 1];
+                if (has_y && actY) {
+#pragma unroll
+                    for (int q = 0; q < Y_EARLY; ++q) {
+                        float v[NY];
+#pragma unroll
+                        for (int i = 0; i < NY; ++i) v[i] = er[q * NY + i];
+                        box_sums<HH, G::SY>(v, S[q]);
+                    }
+#pragma unroll
+                    for (int q = Y_EARLY; q < Y_EARLY + Y_MID; ++q) {
+                        float v[NY];
+                        lds_row(Xs + q * G::XP + y_xo, v);
+#pragma unroll
+                        for (int i = 0; i < NY; ++i) em[(q - Y_EARLY) * NY + i] = v[i];
+                    }
+                }
+                f_cols(rc, std::true_type{}, std::integral_constant<int, 1>{}, std::integral_constant<int, J>{});
+                f_pref(zi, zoff);
+                if (has_y && actY) {
+#pragma unroll
+                    for (int q = Y_EARLY; q < 5; ++q) {
+                        float v[NY];
+                        if (q < Y_EARLY + Y_MID) {
+#pragma unroll
+                            for (int i = 0; i < NY; ++i) v[i] = em[(q < Y_EARLY + Y_MID ? q - Y_EARLY : 0) * NY + i];
+                        } else {
+                            lds_row(Xs + q * G::XP + y_xo, v);
+                        }
+                        box_sums<HH, G::SY>(v, S[q]);
+                    }
+                }
+            } else {
+                f_sums(rc, std::integral_constant<bool, F_STORE_AT_ONCE>{}, zi, zoff);
+            }
+            if (Y_MID > 0 && has_y && actY) {
+                // box sums done above
+            } else if (has_y && actY) {
 #pragma unroll
                 for (int q = 0; q < 5; ++q) {
                     float v[NY];
