@@ -391,7 +391,8 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     //    runs while they arrive, then
     //    the Y lanes read their other rows and form the five box sums, which stay in registers
     //    until P1, and the AX lanes their sums; AZ's z-sums and the gradient come last. At k = 9
-    //    (two rings of 9 planes) nothing is read early and Y's rows are read one at a time. (At
+    //    (two rings of 9 planes) nothing is read before F, one row between F's two columns, and
+    //    the others one at a time after F. (At
     //    k = 7 the AX row read before F measured 1% slower than after it.)
     //  * P1: the Y lanes turn their box sums into ncc and the adjoint coefficients (arithmetic
     //    only, no LDS reads: it keeps the SIMDs busy while the rows of the X and AYs units, on the
@@ -400,7 +401,8 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     constexpr bool F_STORE_AT_ONCE = Y_EARLY < 5;
     // k = 7 (fp32): the box sums of the early rows are formed between F's two columns, and the
     // registers they free take Y_MID more rows, read before F's second column; the rest after F
-    constexpr int Y_MID = (HH == 3 && !BF16 && J == 2) ? 1 : 0;
+    // (1% faster than all three after F). k = 9 reads one row there too (0.6-1% faster).
+    constexpr int Y_MID = ((HH == 3 && !BF16) || HH == 4) && J == 2 ? 1 : 0;
     static_assert(Y_EARLY + Y_MID <= 5, "Y rows");
     constexpr bool AX_EARLY = HH <= 2;                        // the AX row read before F
     constexpr int NY = G::SY + 2 * HH, NA = G::SA + 2 * HH, NX = G::SX + 2 * HH, NB = G::SB + 2 * HH;
