@@ -399,10 +399,12 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     //    other waves, arrive), then the X and AYs units.
     constexpr int Y_EARLY = HH <= 2 ? 5 : HH == 3 ? (BF16 ? 2 : 3) : 0;   // Y rows read before F
     constexpr bool F_STORE_AT_ONCE = Y_EARLY < 5;
-    // k = 7 (fp32): the box sums of the early rows are formed between F's two columns, and the
-    // registers they free take Y_MID more rows, read before F's second column; the rest after F
-    // (1% faster than all three after F). k = 9 reads one row there too (0.6-1% faster).
-    constexpr int Y_MID = ((HH == 3 && !BF16) || HH == 4) && J == 2 ? 1 : 0;
+    // Y_MID of Y's rows are read between F's two columns, after the box sums of the early rows
+    // (whose registers they take); the rest after F. k = 9: one row (0.6-1% faster than none).
+    // k = 7: one row measured 0.7% faster at (2,16,128^3) but 1.3% slower at (2,16,256^3), whose
+    // re-reads of the output planes then missed the L2 more often (HBM reads 1.05x -> up to 1.46x
+    // the inputs, growing from launch to launch); none.
+    constexpr int Y_MID = HH == 4 && J == 2 ? 1 : 0;
     static_assert(Y_EARLY + Y_MID <= 5, "Y rows");
     constexpr bool AX_EARLY = HH <= 2;                        // the AX row read before F
     constexpr int NY = G::SY + 2 * HH, NA = G::SA + 2 * HH, NX = G::SX + 2 * HH, NB = G::SB + 2 * HH;
