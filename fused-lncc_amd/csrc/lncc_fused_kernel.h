@@ -455,9 +455,11 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 for (int i = 0; i < NA; ++i) er[i] = v[i];
             }
             float S[5][G::SY];  // Y's box sums, carried into P1
+            float em[Y_MID > 0 ? Y_MID * NY : 1];
             if constexpr (Y_MID > 0) {
+                // F's first column; then the box sums of the early rows and the reads of the mid
+                // rows; then F's second column and the prefetch
                 f_cols(rc, std::true_type{}, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
-                float em[Y_MID > 0 ? Y_MID * NY : 1];
                 if (has_y && actY) {
 #pragma unroll
                     for (int q = 0; q < Y_EARLY; ++q) {
@@ -467,40 +469,29 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                         box_sums<HH, G::SY>(v, S[q]);
                     }
 #pragma unroll
-                    for (int q = Y_EARLY; q < Y_EARLY + Y_MID; ++q) {
+                    for (int q = 0; q < Y_MID; ++q) {
                         float v[NY];
-                        lds_row(Xs + q * G::XP + y_xo, v);
+                        lds_row(Xs + (Y_EARLY + q) * G::XP + y_xo, v);
 #pragma unroll
-                        for (int i = 0; i < NY; ++i) em[(q - Y_EARLY) * NY + i] = v[i];
+                        for (int i = 0; i < NY; ++i) em[q * NY + i] = v[i];
                     }
                 }
                 f_cols(rc, std::true_type{}, std::integral_constant<int, 1>{}, std::integral_constant<int, J>{});
                 f_pref(zi, zoff);
-                if (has_y && actY) {
-#pragma unroll
-                    for (int q = Y_EARLY; q < 5; ++q) {
-                        float v[NY];
-                        if (q < Y_EARLY + Y_MID) {
-#pragma unroll
-                            for (int i = 0; i < NY; ++i) v[i] = em[(q < Y_EARLY + Y_MID ? q - Y_EARLY : 0) * NY + i];
-                        } else {
-                            lds_row(Xs + q * G::XP + y_xo, v);
-                        }
-                        box_sums<HH, G::SY>(v, S[q]);
-                    }
-                }
             } else {
                 f_sums(rc, std::integral_constant<bool, F_STORE_AT_ONCE>{}, zi, zoff);
             }
-            if (Y_MID > 0 && has_y && actY) {
-                // box sums done above
-            } else if (has_y && actY) {
+            if (has_y && actY) {
+                // the rows not yet summed: early rows (held in er), mid rows (em), the rest read now
 #pragma unroll
-                for (int q = 0; q < 5; ++q) {
+                for (int q = Y_MID > 0 ? Y_EARLY : 0; q < 5; ++q) {
                     float v[NY];
                     if (q < Y_EARLY) {
 #pragma unroll
                         for (int i = 0; i < NY; ++i) v[i] = er[(q < Y_EARLY ? q : 0) * NY + i];
+                    } else if (q < Y_EARLY + Y_MID) {
+#pragma unroll
+                        for (int i = 0; i < NY; ++i) v[i] = em[(q < Y_EARLY + Y_MID ? q - Y_EARLY : 0) * NY + i];
                     } else {
                         lds_row(Xs + q * G::XP + y_xo, v);
                     }

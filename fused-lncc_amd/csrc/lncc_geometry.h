@@ -78,6 +78,9 @@ struct Geo {
     // SIMD w % 4): the AX waves go to the SIMDs with fewer Y waves, which evens out P0.
     static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, UB = 3 * BITEMS;
     static constexpr int NYW = cdiv(YITEMS, 64), XL0 = 64 * NYW, BL0 = rup64(XL0 + UX), NAW = cdiv(UA, 64);
+    // Y items, X units and AYs units on disjoint lanes (the kernel keeps a Y item's offsets in the
+    // registers of the X / AYs unit offsets at k = 7)
+    static_assert(XL0 >= YITEMS && BL0 >= XL0 + UX, "lane kinds");
     static_assert(BL0 + UB <= NT && NAW <= 4 && (NYW == 5 || NYW == 6) && BPOS == 32 && TX == 32 &&
                       NIN <= 2 * NT && TY <= TY_MAX,
                   "lanes");
