@@ -3,10 +3,14 @@
 correlated inputs and zero slabs after signal; the parity bar of tests/test_gpu_sweep.py.
 Not collected by pytest (minutes per 10,000 cases); prints one line per failing case.
 usage: python tests/gpu_sweep_large.py N SEED"""
-import random, sys, time
+import os
+import random
+import sys
+import time
+
 import numpy as np
 import torch
-import os
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 for sub in ("fused-lncc_amd", "oracle", os.path.join("tests", "golden")):
     sys.path.insert(0, os.path.join(ROOT, sub))
