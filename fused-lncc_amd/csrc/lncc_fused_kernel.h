@@ -387,13 +387,12 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // between the issue of another stage's LDS reads and their use hides part of their latency.
     //  * P0: AZ's xy-sums are read first. The Y lanes read Y_EARLY of their five rows (all five
     //    at k <= 5, three at k = 7, two for bf16 at k = 7: more rows held across F exceed the
-    //    128-register budget of a 1024-lane workgroup) and at k <= 5 the AX lanes their row, F
-    //    runs while they arrive, then
-    //    the Y lanes read their other rows and form the five box sums, which stay in registers
-    //    until P1, and the AX lanes their sums; AZ's z-sums and the gradient come last. At k = 9
-    //    (two rings of 9 planes) nothing is read before F, one row between F's two columns, and
-    //    the others one at a time after F. (At
-    //    k = 7 the AX row read before F measured 1% slower than after it.)
+    //    128-register budget of a 1024-lane workgroup) and at k <= 5 the AX lanes their row; F
+    //    runs while they arrive, then the Y lanes read their other rows and form the five box
+    //    sums, which stay in registers until P1, and the AX lanes their sums; AZ's z-sums and the
+    //    gradient come last. At k = 9 (two rings of 9 planes) nothing is read before F, one row
+    //    between F's two columns, and the others one at a time after F. (At k = 7 the AX row read
+    //    before F measured 1% slower than after it.)
     //  * P1: the Y lanes turn their box sums into ncc and the adjoint coefficients (arithmetic
     //    only, no LDS reads: it keeps the SIMDs busy while the rows of the X and AYs units, on the
     //    other waves, arrive), then the X and AYs units.
