@@ -2,11 +2,13 @@
 //   * box_kernel     zero-padded k^3 box-sum of one fp32 field (the reference's box3d_sep test hook,
 //                    fused_lncc/csrc/lncc3d.cu:286-344), or the reference's backward combine
 //                    grad = scale (box A + 2p box Bc + t box Cc) from materialized fp32 maps
-//                    (lncc3d.cu:163-235). Plane-marching: LDS x/y passes, z running sums in registers.
+//                    (lncc3d.cu:163-235). Plane-marching: direct k-tap x/y sums in LDS, z window sums
+//                    from a register ring (lncc_window.h), each window a sum of its own values only.
 //   * finalize_kernel  loss = 1 - (sum of workgroup partials)/M, summed in a fixed order (float64).
 //   * scale_kernel   grad *= grad_out, skipped on the device when grad_out == 1 (no host sync).
 #include "lncc_common.h"
 #include "lncc_launch.h"
+#include "lncc_window.h"
 
 namespace fl {
 
@@ -34,10 +36,13 @@ __global__ __launch_bounds__(BNT) void box_kernel(BoxArgs a) {
     const int x0 = tx * BT, y0 = ty * BT;
     const float* fld[3] = {a.f0, a.f1, a.f2};
 
-    float ring[NF][K], zsum[NF];
+    // per field: the xy-sums of the last k planes (ring slot = the plane's position in its block of
+    // k) and the prefix sum of the current block; the z-sum of a window is that prefix plus the
+    // previous block's suffix from the ring, so a window of zeros sums to exactly zero
+    float ring[NF][K], zpre[NF], zsum[NF];
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-        zsum[f] = 0.f;
+        zpre[f] = 0.f;
 #pragma unroll
         for (int r = 0; r < K; ++r) ring[f][r] = 0.f;
     }
@@ -73,8 +78,7 @@ __global__ __launch_bounds__(BNT) void box_kernel(BoxArgs a) {
                 float s = 0.f;
 #pragma unroll
                 for (int d = 0; d < K; ++d) s += xsum[f][oy + d][ox];
-                zsum[f] += s - ring[f][r];
-                ring[f][r] = s;
+                zsum[f] = zstep1<K, r>(s, zpre[f], ring[f]);
             }
             const int zo = zi - HH;
             const int gx = x0 + ox, gy = y0 + oy;

@@ -57,6 +57,8 @@ Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     const int ty = fl::tile_rows(halo);
     p.ntx = (int)((W + fl::TX - 1) / fl::TX);
     p.nty = (int)((H + ty - 1) / ty);
+    // callers pass shapes that passed check_grid, so base < 2^32 / NT; a forced chunk length can
+    // multiply it by up to D <= 2^30, which still fits int64
     const int64_t base = B * p.ntx * p.nty;
     // Split D into nzc chunks. A chunk of d planes costs d + 4h + 3 pipeline steps, and the
     // workgroups run in rounds of one per CU: pick the split with the fewest rounds x steps (ties:
@@ -94,11 +96,24 @@ int check_shape(int64_t B, int64_t D, int64_t H, int64_t W, int elem) {
     return FL_OK;
 }
 
+// B x ntx x nty workgroups, or -1 if the product does not fit int64 (check_shape allows B up to
+// 2^40 and planes of up to 2^30 columns, whose product can exceed 2^63).
+int64_t workgroups(int64_t B, int64_t ntx, int64_t nty) {
+    int64_t plane = 0, n = 0;
+    if (__builtin_mul_overflow(ntx, nty, &plane) || __builtin_mul_overflow(plane, B, &n)) return -1;
+    return n;
+}
+
+// Tiles of the fused kernel: B x (W/TX) x (H/TY).
+int64_t tile_count(int64_t B, int64_t H, int64_t W, int halo) {
+    return workgroups(B, (W + fl::TX - 1) / fl::TX, (H + fl::tile_rows(halo) - 1) / fl::tile_rows(halo));
+}
+
 // The fused kernel's smallest plan (one workgroup per tile and volume, D unsplit) must fit one
-// launch; the products stay far inside int64 after check_shape's limits.
+// launch.
 int check_grid(int64_t B, int64_t H, int64_t W, int halo) {
-    const int64_t tiles = B * ((W + fl::TX - 1) / fl::TX) * ((H + fl::tile_rows(halo) - 1) / fl::tile_rows(halo));
-    if (!grid_fits(tiles, fl::NT)) return fail(FL_E_SHAPE, "fused_lncc: too many volumes/tiles for one launch");
+    if (!grid_fits(tile_count(B, H, W, halo), fl::NT))
+        return fail(FL_E_SHAPE, "fused_lncc: too many volumes/tiles for one launch");
     return FL_OK;
 }
 
@@ -143,7 +158,7 @@ fl::FusedArgs fused_args(const void* pred, const void* target, int64_t B, int64_
     a.inv_n = (float)(1.0 / n);
     a.nf = (float)n;
     a.ndr = (float)n * smooth_dr;
-    a.gscale = (float)(2.0 * n / M);
+    a.gscale = (float)(2.0 * n / M) * fl::range_scale(kernel_size);   // a power of two: exact
     return a;
 }
 
@@ -379,7 +394,8 @@ int fl_lncc_backward(const float* A, const float* Bc, const float* Cc, const voi
     a.ntx = (int)((W + 15) / 16);
     a.nty = (int)((H + 15) / 16);
     a.scale = scale;
-    if (!grid_fits(B * a.ntx * a.nty, fl::kBoxLanes)) return fail(FL_E_SHAPE, "fl_lncc_backward: too many volumes/tiles for one launch");
+    if (!grid_fits(workgroups(B, a.ntx, a.nty), fl::kBoxLanes))
+        return fail(FL_E_SHAPE, "fl_lncc_backward: too many volumes/tiles for one launch");
     const uint32_t nb = (uint32_t)(B * a.ntx * a.nty);
     hipError_t e = fl::launch_box(kernel_size / 2, 3, dtype == FL_BF16, a, nb, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "fl_lncc_backward: launch");
@@ -399,7 +415,8 @@ int fl_box3d(const float* x, float* y, int64_t B, int64_t D, int64_t H, int64_t 
     a.ntx = (int)((W + 15) / 16);
     a.nty = (int)((H + 15) / 16);
     a.scale = 1.f;
-    if (!grid_fits(B * a.ntx * a.nty, fl::kBoxLanes)) return fail(FL_E_SHAPE, "fl_box3d: too many volumes/tiles for one launch");
+    if (!grid_fits(workgroups(B, a.ntx, a.nty), fl::kBoxLanes))
+        return fail(FL_E_SHAPE, "fl_box3d: too many volumes/tiles for one launch");
     const uint32_t nb = (uint32_t)(B * a.ntx * a.nty);
     hipError_t e = fl::launch_box(kernel_size / 2, 1, false, a, nb, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "fl_box3d: launch");

@@ -46,6 +46,15 @@
 // division by dr^2 blows up). With r = 1/(VP VT), c = X r, u = c VT, w = St - Sp u it carries
 //   alpha = c w, beta = c u, gamma = c   (A = -2 alpha, Bc = -n beta, Cc = 2 n gamma)
 // so that grad = (2n/M) (box(alpha)/n + p box(beta) - t box(gamma)).
+// Range: VP VT = n^2 vp vt would overflow n^2 times earlier than the reference's vp vt (at a
+// local standard deviation ~20x smaller at k = 7). The kernel therefore forms VT s instead of VT,
+// with s = 2^-E the power of two just below 1/n^2, so that r and c carry a factor 1/s; ncc is
+// formed as (X s) (c/s), and alpha, beta, gamma carry 1/s, which the gradient's final scale (2n/M)
+// s takes back. Each is one multiply by a literal per voxel (on gfx9 a select or an fma with a
+// non-inline constant would need a vector register, and at k >= 5 the kernels are at the
+// register limit). Scaling by a power of two is exact, so every result is bit for bit what the
+// unscaled arithmetic gives wherever that does not overflow, and VP VT s overflows only where the
+// reference's vp vt does (n^2 s lies in (1/2, 1]).
 #pragma once
 #include "lncc_common.h"
 #include "lncc_launch.h"
@@ -258,6 +267,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 
     double loss_acc = 0.0;
     const float inv_n = a.inv_n, nf = a.nf, ndr = a.ndr;
+    constexpr float VS = range_scale(K);   // the range scale s = 2^-E (header)
 
     // Plane addresses advance by one plane per step: zoff = zi * plane size, and every plane the
     // loop touches sits at a fixed plane distance from zi. A plane outside its valid range gets a
@@ -293,10 +303,10 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             // would break that rounding's ties (frequent when n Spp has few significant bits)
             // always upwards, a bias of ~2e-5 in ncc on offset intensities at k = 3
             const float VP = fmaxf(fmaf(-Sp, Sp, nf * Spp), 0.f) + ndr;
-            const float VT = fmaxf(fmaf(-St, St, nf * Stt), 0.f) + ndr;
+            const float VT = (fmaxf(fmaf(-St, St, nf * Stt), 0.f) + ndr) * VS;   // VT s
             const float rr = __builtin_amdgcn_rcpf(VP * VT);
-            const float cr = X * rr;
-            const float ncc = X * cr;
+            const float cr = X * rr;             // c / s
+            const float ncc = (X * VS) * cr;     // ncc
             const bool live = y_inv[i] && (ncc < 1.0f);
             const float nccc = (ncc >= 1.0f) ? 1.0f : ncc;
             if (count && y_core[i]) lsum += nccc;
@@ -323,9 +333,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                     const int64_t o = ((b * D + zcY) * Hd + gy) * (int64_t)Wd + gx;
                     a.ncc_map[o] = nccc;
                     if (a.a_map) {  // null: the ncc map alone
-                        a.a_map[o] = live ? -2.f * (cr * w) : 0.f;
-                        a.b_map[o] = live ? -nf * (cr * uu) : 0.f;
-                        a.c_map[o] = live ? (2.f * nf) * cr : 0.f;
+                        a.a_map[o] = live ? (-2.f * VS) * (cr * w) : 0.f;
+                        a.b_map[o] = live ? (-nf * VS) * (cr * uu) : 0.f;
+                        a.c_map[o] = live ? (2.f * nf * VS) * cr : 0.f;
                     }
                 }
             }
@@ -521,7 +531,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
 #pragma unroll
                 for (int c = 0; c < 3; ++c) gw[c] = zstep1<K, r, A_CHAIN>(ys[c], gpre[c], gring[c]);
                 const int zo = zi - ZO;
-                const float g = a.gscale * fmaf(inv_n, gw[0], fmaf(pz, gw[1], -tzz * gw[2]));
+                const float g = a.gscale * fmaf(inv_n, gw[0], fmaf(pz, gw[1], -tzz * gw[2]));   // gscale holds s
                 // Non-temporal: the gradient is never read back, and this re-read of p,t is the
                 // last use of those lines. With the default policy both would be promoted in the
                 // L2 and push out the planes that F loaded and this stage re-reads 2h+3 steps

@@ -22,6 +22,16 @@ constexpr int TY_MAX = 32;
 FL_HD constexpr int tile_rows(int halo) { return halo >= 4 ? 24 : 32; }
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+// The power of two 2^-E with 2^E the smallest power of two >= n^2, n = k^3: the factor by which the
+// fused kernel scales VT so that VP VT stays within the float range wherever the reference's
+// vp vt does (VP VT = n^2 vp vt; n^2 2^-E lies in (1/2, 1]).
+FL_HD constexpr float range_scale(int k) {
+    const long long n2 = (long long)k * k * k * k * k * k;
+    float s = 1.0f;
+    for (long long p = 1; p < n2; p *= 2) s *= 0.5f;
+    return s;
+}
 constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 constexpr int odd(int a) { return a | 1; }
 

@@ -19,7 +19,7 @@ struct FusedArgs {
     int dimD, dimH, dimW;
     int ntx, nty, nzc, dchunk;
     float inv_n, nf, ndr;     // 1/n, n = k^3 and n * smooth_dr as float32
-    float gscale;             // 2 n / M
+    float gscale;             // (2 n / M) s, s = range_scale(k) (the kernel's adjoints carry 1/s)
 };
 
 struct BoxArgs {

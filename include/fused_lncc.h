@@ -78,10 +78,14 @@ int fl_lncc_loss_grad(const void* pred, const void* target, int dtype, int64_t B
  * until the process ends), so the call makes no hipMalloc/hipFree and no allocating library call.
  * No counterpart in the reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation). Limit: launches of at most
- * 65536 workgroups (fl_workspace_bytes(...) <= 512 KiB, e.g. up to 32 volumes of 512^3 at k = 7);
- * larger ones return FL_E_WORKSPACE. Every call on one GPU shares that GPU's scratch: calls that
- * overlap on one GPU (other streams, other threads) race and must be serialized by the caller.
- * Results are bit-identical to fl_lncc_loss_grad's.
+ * 65536 workgroups, i.e. fl_workspace_bytes(...) <= 512 KiB on the target device (e.g. up to 256
+ * volumes of 512^3 at k = 7; the workgroup count of small volumes follows the device's compute-unit
+ * count, so check fl_workspace_bytes rather than a rule of thumb); larger ones return
+ * FL_E_WORKSPACE. The first call on each device looks up the scratch array's device address
+ * (hipGetSymbolAddress), which must not happen inside a HIP graph capture: make one call on each
+ * device before capturing. Every call on one GPU shares that GPU's scratch: calls that overlap on
+ * one GPU (other streams, other threads) race and must be serialized by the caller. Results are
+ * bit-identical to fl_lncc_loss_grad's.
  */
 int fl_lncc_loss_grad_noalloc(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,
                               int64_t W, int kernel_size, float smooth_dr, float* loss, void* grad, void* stream);
@@ -90,7 +94,10 @@ int fl_lncc_loss_grad_noalloc(const void* pred, const void* target, int dtype, i
  * The two launches of fl_lncc_loss_grad, for callers that time or schedule them separately:
  * fl_lncc_fused_partials runs the fused kernel alone (gradient when grad != NULL, one float64 ncc
  * partial sum per workgroup into `workspace`); fl_lncc_finalize reduces those partials in a fixed
- * order into *loss = 1 - sum/M. Same shape arguments as fl_lncc_loss_grad.
+ * order into *loss = 1 - sum/M. Same shape arguments as fl_lncc_loss_grad. Both re-plan the launch
+ * from the shape, so call them from the same host thread when fl_test_set_dchunk is in effect (its
+ * chunk override is per thread; a finalize planned without it would read a different number of
+ * partials).
  */
 int fl_lncc_fused_partials(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,
                            int64_t W, int kernel_size, float smooth_dr, void* grad, void* workspace,

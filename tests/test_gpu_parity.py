@@ -16,6 +16,7 @@ import torch.nn.functional as F
 
 import oracle as O
 import workloads as wl
+from checks import assert_grad_bf16, cos_rel
 from fused_lncc import ext, fused_lncc_loss
 
 pytestmark = pytest.mark.gpu
@@ -43,33 +44,9 @@ def fused(p, t, k, dr=1e-5, dtype=None):
     return float(loss.item()), pd.grad.double().cpu().numpy(), pd.grad.dtype
 
 
-def cos_rel(g, gr):
-    g = np.asarray(g, np.float64).ravel()
-    gr = np.asarray(gr, np.float64).ravel()
-    n = np.linalg.norm(gr)
-    return float(g @ gr / (np.linalg.norm(g) * n)), float(np.linalg.norm(g - gr) / n)
-
-
 def assert_grad(g, gr, cos_min=GRAD_COS, rel_max=GRAD_REL_L2):
     c, r = cos_rel(g, gr)
     assert c > cos_min and r < rel_max, f"cos={c:.8f} relL2={r:.3e}"
-
-
-def assert_grad_bf16(g, gr):
-    """A bfloat16 gradient against the float32 oracle gradient of the same (bf16-representable)
-    inputs: the kernel accumulates in float32 and rounds once to nearest even, so the gradient is
-    the oracle's rounded to bf16 up to the float32 error: within one bf16 ulp of round_bf16(oracle)
-    everywhere (plus 1e-5 of the gradient's scale for elements near zero), relative L2 error <=
-    3e-3 (one rounding to 8 significant bits costs ~1.1e-3) and cosine > 0.9999. The reference's
-    own bf16 checks are looser (tests/test_bf16.py:10-21)."""
-    g = np.asarray(g, np.float64).ravel()
-    gr = np.asarray(gr, np.float64).ravel()
-    c, r = cos_rel(g, gr)
-    assert c > 0.9999 and r <= 3e-3, f"bf16 gradient cos={c:.8f} relL2={r:.3e}"
-    rb = O.round_bf16_np(gr).astype(np.float64)
-    tol = O.bf16_ulp(rb) + 1e-5 * np.abs(gr).max()
-    bad = np.abs(g - rb) > tol
-    assert not bad.any(), f"{bad.sum()} of {bad.size} bf16 gradient elements more than one ulp from the rounded oracle"
 
 
 def assert_loss(l, lr, rtol):
@@ -186,6 +163,62 @@ def test_lncc_map(k, dtype):
     if dtype == torch.float32:
         _, _, om = O.lncc(p.numpy(), t.numpy(), k, grad=False, maps=True)
         assert np.abs(m.double().cpu().numpy() - om["ncc"]).max() < 1e-3
+
+
+def _pure_windows(x, fill, k):
+    """Voxels whose zero-padded k^3 window holds no in-volume value other than ``fill``."""
+    return O.box3d((np.asarray(x) != fill).astype(np.float64), k) == 0
+
+
+@pytest.mark.parametrize("k", [3, 5, 7, 9])
+@pytest.mark.parametrize("fill", [0.0, 0.5])
+def test_box3d_exact_after_signal(k, fill):
+    """box3d_sep_forward on U[0,1) signal followed by a zero or constant slab along D (the box
+    kernel marches all of D) and one along W: a window that holds only the fill value sums to
+    exactly what the reference's direct k-tap sums give, 0 or (number of in-volume voxels) * 0.5
+    (every partial sum of up to 729 halves is a float), so it equals the float64 oracle bit for
+    bit; elsewhere within float32 rounding (lncc3d.cu:203-230, 308-325)."""
+    x = torch.rand(2, 60, 21, 37, generator=torch.Generator().manual_seed(40 + k))
+    x[:, 30:] = fill
+    x[:, :, :, 25:] = fill
+    y = ext.box3d_sep_forward(x.to(DEV), k).double().cpu().numpy()
+    yr = O.box3d(x.numpy(), k)
+    pure = _pure_windows(x.numpy(), fill, k)
+    assert pure.sum() > 1000
+    bad = y[pure] != yr[pure]
+    assert not bad.any(), f"{bad.sum()} of {pure.sum()} single-valued windows differ (max {np.abs(y[pure] - yr[pure]).max():.3e})"
+    assert np.abs(y - yr).max() < 1e-4 * np.abs(yr).max()
+
+
+@pytest.mark.parametrize("k", [3, 5, 7, 9])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_reference_backward_exact_after_signal(k, dtype):
+    """The reference's two-kernel path, lncc_forward then lncc_backward with scale -1/M
+    (fused_lncc/__init__.py:62-73), on [0, 255] integer data with a zero slab along D and a
+    constant slab (128) along W after signal: the gradient is exactly zero wherever the float64
+    oracle's is (deep inside either slab every window is single-valued, so cross = 0, var = 0 and
+    the adjoints vanish, as with the reference's direct sums), and within the parity bar (bf16:
+    one ulp of the rounded oracle) everywhere."""
+    shape = (1, 2, 40, 22, 36)
+    p, t = wl.structured_pair(shape, "byte", 60 + k, axis=2, start=24, fill=0.0)
+    p[..., 28:] = 128.0
+    t[..., 28:] = 128.0
+    B = shape[0] * shape[1]
+    pf = p.reshape(B, *shape[2:]).to(dtype).to(DEV)
+    tf = t.reshape(B, *shape[2:]).to(dtype).to(DEV)
+    _, A, Bc, Cc = ext.lncc_forward(pf, tf, k, 1e-5)
+    got = ext.lncc_backward(A, Bc, Cc, pf, tf, k, -1.0 / p.numel())
+    assert got.dtype == dtype
+    g = got.double().cpu().numpy().reshape(shape)
+    _, g64 = O.lncc(p.numpy(), t.numpy(), k)
+    g64 = g64.astype(np.float64).reshape(shape)
+    zero = g64 == 0
+    assert zero.sum() > 1000
+    assert np.count_nonzero(g[zero]) == 0, f"{np.count_nonzero(g[zero])} of {zero.sum()} exact-zero gradient voxels are not zero"
+    if dtype == torch.float32:
+        assert_grad(g, g64)
+    else:
+        assert_grad_bf16(g, g64)
 
 
 @pytest.mark.parametrize("k", [3, 5, 7, 9])

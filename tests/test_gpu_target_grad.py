@@ -7,6 +7,7 @@ import torch
 
 import torch_lncc_port
 import workloads as wl
+from checks import assert_grad_bf16
 from fused_lncc import fused_lncc_loss
 
 pytestmark = pytest.mark.gpu
@@ -57,10 +58,10 @@ def test_target_grad_alone_bf16_and_retained_graph():
     td.grad = None
     loss.backward()                                 # second backward through the retained graph
     assert g1.dtype == torch.bfloat16 and pd.grad is None
-    c, rel = _cos_rel(g1.float(), 2.0 * gt_ref)
-    assert c > 0.999 and rel < 2e-2, (c, rel)
-    c, rel = _cos_rel(td.grad.float(), gt_ref)
-    assert c > 0.999 and rel < 2e-2, (c, rel)
+    # float32 arithmetic rounded once to bf16 (the scale by 2 is exact): within one bf16 ulp of
+    # the rounded float64 gradient, as for the pred gradient
+    assert_grad_bf16(g1.double().cpu().numpy(), (2.0 * gt_ref).numpy())
+    assert_grad_bf16(td.grad.double().cpu().numpy(), gt_ref.numpy())
 
 
 def test_target_grad_compiled_matches_eager():
@@ -104,6 +105,5 @@ def test_dual_kernel_against_single_passes(k, dt, dchunk, force_dchunk):
     assert gp.dtype == dt and gt.dtype == dt
     assert torch.equal(gp, gp1)
     assert loss.item() == loss1.item()
-    tol = 1e-6 if dt == torch.float32 else 1e-2
-    c, rel = _cos_rel(gt.float(), gt1.float())
-    assert c > 1 - tol and rel < 10 * tol, (c, rel)
+    # the same kernel on the same (swapped) inputs and the same plan: bit for bit
+    assert torch.equal(gt, gt1)

@@ -112,6 +112,14 @@ def test_shape_limits_without_overflow():
     # B x tiles x D would overflow int64
     assert lib.fl_validate(_lib.FL_F32, 7, 2 ** 62, 2 ** 30, 64, 64) == _lib.FL_E_SHAPE
     assert "too many" in lib.fl_last_error().decode()
+    # B x tiles alone can exceed int64: bf16 planes of 1 x 1073740448 columns hold 33554389 tiles
+    # of 32 columns, and 549756518401 (< 2^40) such volumes make 2^64 + 3260373 tiles, which a plain
+    # int64 product wraps to a small positive count that would pass the grid limit
+    assert lib.fl_validate(_lib.FL_BF16, 7, 549756518401, 1, 1, 1073740448) == _lib.FL_E_SHAPE
+    assert "too many" in lib.fl_last_error().decode()
+    assert lib.fl_workspace_bytes(549756518401, 1, 1, 1073740448, 7) == 0
+    # the box kernels' 16-column tiles: 67108778 per such plane of 1073740448 / 2 columns (fp32)
+    assert lib.fl_box3d(8, 8, 549756518401, 1, 1, 536870224, 7, None) == _lib.FL_E_SHAPE
     # the debug box-sum path has 16 x 16 tiles: a grid of 2^26 x 8 x 8 workgroups is refused on the
     # host (nothing is launched)
     assert lib.fl_box3d(8, 8, 2 ** 26, 1, 128, 128, 7, None) == _lib.FL_E_SHAPE

@@ -70,3 +70,46 @@ def test_no_alloc_loss_only():
                                              loss.data_ptr(), None, _stream()))
     torch.cuda.synchronize()
     assert torch.equal(loss, l_ws)
+
+
+def test_no_alloc_under_graph_capture():
+    """The entry point captured into a HIP graph (after one eager call on the device, which looks up
+    the scratch address outside the capture): every replay, with new inputs copied into the static
+    buffers and eager library calls between the replays (which reuse the same scratch), equals the
+    workspace entry point on the same inputs bit for bit."""
+    lib = _lib.load()
+    shape, k = (4, 24, 40, 44), 7
+    B, D, H, W = shape
+    pf = torch.empty(shape, device=DEV)
+    tf = torch.empty(shape, device=DEV)
+    loss = torch.empty((), dtype=torch.float32, device=DEV)
+    grad = torch.empty_like(pf)
+
+    def load(i):
+        p, t = wl.randn_pair(shape, 300 + i)
+        pf.copy_(0.5 * t + 0.5 * p)
+        tf.copy_(t)
+
+    def call():
+        _lib.check(lib.fl_lncc_loss_grad_noalloc(pf.data_ptr(), tf.data_ptr(), _lib.FL_F32, B, D, H, W, k, 1e-5,
+                                                 loss.data_ptr(), grad.data_ptr(), _stream()))
+
+    load(0)
+    call()   # eager: the scratch lookup happens here, outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for i in range(1, 5):
+        print(f"no-alloc graph replay {i}", flush=True)
+        load(i)
+        g.replay()
+        torch.cuda.synchronize()
+        got_l, got_g = loss.clone(), grad.clone()
+        l_ws, g_ws = _with_workspace(pf, tf, _lib.FL_F32, k)
+        # an eager allocation-free call on another shape in between: it overwrites the scratch
+        small = torch.randn(2, 9, 20, 24, device=DEV)
+        _no_alloc(small, small.flip(-1).contiguous(), _lib.FL_F32, 5)
+        torch.cuda.synchronize()
+        assert torch.equal(got_l, l_ws), (got_l.item(), l_ws.item())
+        assert torch.equal(got_g, g_ws)
