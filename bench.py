@@ -6,8 +6,8 @@ headline workload (2,16,128,128,128) fp32, k=7 (target ~ N(0,1) seed 0, pred = 0
 
 * value / unit: algorithmic HBM throughput of the whole step, 12 B per voxel (read pred, read
   target, write grad once) / ms_per_step, in GB/s;
-* roofline: the fused kernel alone (lncc_fused_kernel), timed with HIP events on the stream it is
-  launched on, against the 8 TB/s HBM peak; traffic = FETCH_SIZE + WRITE_SIZE per launch from the
+* roofline: the fused kernel alone (lncc_fused_kernel; lncc_small_kernel for volumes of at most
+  16^3), timed with HIP events on the stream it is launched on, against the 8 TB/s HBM peak; traffic = FETCH_SIZE + WRITE_SIZE per launch from the
   committed rocprofv3 counter summary when present;
 * order: one untimed step (one-time host costs), a clock settle (the fused kernel, untimed, for
   --settle-ms of GPU time), the kernel-only timing, then --warmup untimed steps and exactly
@@ -39,7 +39,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--workload", default="headline", choices=["headline", "bf16", "mri", "large", "cpu"])
+    ap.add_argument("--workload", default="headline",
+                    choices=["headline", "bf16", "mri", "large", "cpu", "feat16", "feat64"])
     ap.add_argument("--kernel-reps", type=int, default=40)
     ap.add_argument("--settle-ms", type=float, default=150.0,
                     help="untimed GPU work (the fused kernel) before anything is timed, so that every "
@@ -78,15 +79,17 @@ def _cpu_model():
 
 def cpu_baseline(workload, k, seconds):
     """The reference's naive PyTorch path (oracle/torch_lncc_port.py) on the host threads torch
-    uses: the whole (1,1,32^3) k=3 case for the cpu workload, otherwise one (N,C) volume of the
-    workload (one 128^3 volume of the headline and bf16 workloads, in fp32; the MRI-shaped volume
-    whole), timed until ``seconds`` of work or 50 runs, median."""
+    uses: the whole (1,1,32^3) k=3 case for the cpu workload, otherwise a sample of the workload's
+    (N,C) volumes (one 128^3 volume of the headline, bf16 and large workloads, in fp32; the
+    MRI-shaped volume whole; 32 of the 256 16^3 volumes of feat16; one 64^3 volume of feat64),
+    timed until ``seconds`` of work or 50 runs, median."""
     import torch
 
     import torch_lncc_port
     import workloads as wl
     spec = wl.WORKLOADS[workload]
-    shape = spec["shape"] if workload in ("cpu", "mri") else (1, 1, 128, 128, 128)
+    sample = {"cpu": spec["shape"], "mri": spec["shape"], "feat16": (1, 32, 16, 16, 16), "feat64": (1, 1, 64, 64, 64)}
+    shape = sample.get(workload, (1, 1, 128, 128, 128))
     p, t = wl.make_inputs(workload, shape)
     p, t = p.float(), t.float()
     for _ in range(2 if workload == "cpu" else 0):   # warm-up of the tiny case
@@ -104,8 +107,9 @@ def cpu_baseline(workload, k, seconds):
     vox = 1
     for n in shape:
         vox *= n
+    nvol = spec["shape"][0] * spec["shape"][1]
     what = "the whole workload" if workload == "cpu" else (
-        "the volume" if workload == "mri" else f"1 of the {spec['shape'][0] * spec['shape'][1]} volumes")
+        "the volume" if workload == "mri" else f"{shape[0] * shape[1]} of the {nvol} volumes")
     threads = torch.get_num_threads()
     return {"value": round(vox * 12 / med / 1e9, 6), "unit": "GB/s", "cores": threads,
             "kind": "port", "ms": round(med * 1e3, 4), "voxels_per_s": round(vox / med, 1),
@@ -242,7 +246,8 @@ def main():
                    "input_dtype": dtname, "bytes_per_voxel": step_bpv, "target_grad": a.target_grad},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
-                     "kernel": "lncc_fused_kernel", "algorithmic_bytes_per_launch": alg_bytes},
+                     "kernel": "lncc_small_kernel" if max(D, H, W) <= 16 else "lncc_fused_kernel",
+                     "algorithmic_bytes_per_launch": alg_bytes},
     }
     if not a.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(a.workload, k, a.cpu_seconds)

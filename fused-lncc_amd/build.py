@@ -20,7 +20,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CFLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 SOURCES = ["lncc_fused_h1.hip", "lncc_fused_h2.hip", "lncc_fused_h3.hip", "lncc_fused_h4.hip",
-           "lncc_aux.hip", "lncc_capi.hip"]
+           "lncc_small.hip", "lncc_aux.hip", "lncc_capi.hip"]
 
 
 def _compile(src):

@@ -30,6 +30,7 @@ constexpr int64_t kMaxPlaneBytes = 0x7fffffffLL;  // per-plane buffer offsets ar
 struct Plan {
     int ntx, nty, nzc, dchunk;
     int64_t nblocks;
+    bool small;   // the small-volume kernel: one workgroup per volume
 };
 
 // Compute units of the current device, read once per device (256 on an MI355X in its
@@ -54,6 +55,15 @@ int device_cus() {
 // long unsplit marches).
 Plan plan_fused(int64_t B, int64_t D, int64_t H, int64_t W, int halo) {
     Plan p;
+    // Volumes of at most 16 x 16 x 16 go to the small-volume kernel (whole volume in LDS, one
+    // workgroup each), unless a test fixes the plane-marching kernel's chunk length.
+    p.small = D <= fl::kSmallEdge && H <= fl::kSmallEdge && W <= fl::kSmallEdge && t_dchunk_override == 0;
+    if (p.small) {
+        p.ntx = p.nty = p.nzc = 1;
+        p.dchunk = (int)D;
+        p.nblocks = B;
+        return p;
+    }
     const int ty = fl::tile_rows(halo);
     p.ntx = (int)((W + fl::TX - 1) / fl::TX);
     p.nty = (int)((H + ty - 1) / ty);
@@ -129,7 +139,9 @@ int check_dtype(int dtype) {
     return FL_OK;
 }
 
-hipError_t launch_fused(int halo, int mode, bool bf16, const fl::FusedArgs& a, uint32_t nb, hipStream_t st) {
+hipError_t launch_fused(int halo, int mode, bool bf16, const fl::FusedArgs& a, const Plan& p, hipStream_t st) {
+    const uint32_t nb = (uint32_t)p.nblocks;
+    if (p.small) return fl::launch_small(halo, mode, bf16, a, nb, st);
     switch (halo) {
         case 1: return fl::launch_fused_h1(mode, bf16, a, nb, st);
         case 2: return fl::launch_fused_h2(mode, bf16, a, nb, st);
@@ -227,8 +239,10 @@ int fl_validate(int dtype, int kernel_size, int64_t B, int64_t D, int64_t H, int
 
 size_t fl_lds_bytes(int kernel_size, int dtype) {
     if (check_k(kernel_size) || check_dtype(dtype)) return 0;
-    // the static LDS of the gradient kernel: the five z-sum and x-sum planes, the three adjoint
-    // planes at each pass, and the per-wave partials of the loss (the same for both dtypes)
+    // the static LDS of the gradient kernels: the plane-marching kernel's five z-sum and x-sum
+    // planes, the three adjoint planes at each pass, and the per-wave partials of the loss (the
+    // same for both dtypes); the small-volume kernel's five 16^3 fields (the first three reused for
+    // the adjoints), three more for the adjoint pass, and its per-wave partials. The larger of the two.
     size_t floats = 0;
     switch (kernel_size / 2) {
         case 1: floats = fl::Geo<1>::LDS_FLOATS; break;
@@ -236,7 +250,10 @@ size_t fl_lds_bytes(int kernel_size, int dtype) {
         case 3: floats = fl::Geo<3>::LDS_FLOATS; break;
         default: floats = fl::Geo<4>::LDS_FLOATS; break;
     }
-    return floats * sizeof(float) + (fl::NT / 64) * sizeof(double);
+    const size_t marching = floats * sizeof(float) + (fl::NT / 64) * sizeof(double);
+    const size_t small = (size_t)8 * fl::kSmallEdge * fl::kSmallEdge * fl::kSmallEdge * sizeof(float) +
+                         (fl::kSmallLanes / 64) * sizeof(double);
+    return marching > small ? marching : small;
 }
 
 size_t fl_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_t W, int kernel_size) {
@@ -262,7 +279,7 @@ int fl_lncc_fused_partials(const void* pred, const void* target, int dtype, int6
     fl::FusedArgs a = fused_args(pred, target, B, D, H, W, kernel_size, smooth_dr, p);
     a.grad = grad;
     a.partials = static_cast<double*>(workspace);
-    hipError_t e = launch_fused(halo, grad ? fl::MODE_GRAD : fl::MODE_LOSS, dtype == FL_BF16, a, (uint32_t)p.nblocks,
+    hipError_t e = launch_fused(halo, grad ? fl::MODE_GRAD : fl::MODE_LOSS, dtype == FL_BF16, a, p,
                                 static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "fl_lncc_fused_partials: fused kernel launch");
     return FL_OK;
@@ -318,7 +335,7 @@ int fl_lncc_loss_grad_noalloc(const void* pred, const void* target, int dtype, i
     a.grad = grad;
     a.partials = part;
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    hipError_t e = launch_fused(halo, grad ? fl::MODE_GRAD : fl::MODE_LOSS, dtype == FL_BF16, a, (uint32_t)p.nblocks, st);
+    hipError_t e = launch_fused(halo, grad ? fl::MODE_GRAD : fl::MODE_LOSS, dtype == FL_BF16, a, p, st);
     if (e != hipSuccess) return hip_fail(e, "fl_lncc_loss_grad_noalloc: fused kernel launch");
     const double M = (double)B * (double)D * (double)H * (double)W;
     e = fl::launch_finalize(part, (int)p.nblocks, 1.0 / M, loss, st);
@@ -369,7 +386,7 @@ int fl_lncc_maps(const void* pred, const void* target, int dtype, int64_t B, int
     a.a_map = A;
     a.b_map = Bc;
     a.c_map = Cc;
-    hipError_t e = launch_fused(halo, fl::MODE_MAPS, dtype == FL_BF16, a, (uint32_t)p.nblocks,
+    hipError_t e = launch_fused(halo, fl::MODE_MAPS, dtype == FL_BF16, a, p,
                                 static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "fl_lncc_maps: launch");
     return FL_OK;

@@ -39,6 +39,12 @@ hipError_t launch_fused_h2(int mode, bool bf16, const FusedArgs& a, uint32_t nbl
 hipError_t launch_fused_h3(int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
 hipError_t launch_fused_h4(int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
 
+// The small-volume kernel (lncc_small.hip): volumes whose D, H and W are all at most kSmallEdge,
+// one workgroup of kSmallLanes lanes per volume (FusedArgs' tile and chunk fields unused).
+constexpr int kSmallEdge = 16;
+constexpr int kSmallLanes = 1024;
+hipError_t launch_small(int halo, int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
+
 // box3d (nfields = 1, fp32 out) and the reference backward combine (nfields = 3): workgroups of
 // kBoxLanes lanes, one per 16 x 16 tile of one volume
 constexpr int kBoxLanes = 256;

@@ -12,6 +12,9 @@ Workloads (pred, target are (N, C, D, H, W)):
 * ``headline`` (2,16,128,128,128) fp32, k=7: target ~ N(0,1) seed 0, pred = 0.8*target + 0.6*N(0,1) seed 1.
 * ``bf16``     the headline recipe at (2,16,128,128,128) built in fp32, cast to bf16, k=5.
 * ``large``    the headline recipe at (2,16,256,256,256) fp32, k=7.
+* ``feat16``   (1,256,16,16,16) fp32, k=7, and ``feat64`` (2,64,64,64,64) fp32, k=7: the reference's other
+  two benchmark shapes (bench.py:52, BENCHMARKS.md:17-18), many channels of small feature volumes;
+  pred, target ~ N(0,1) independent (seeds 0 and 1), as the reference's benchmark draws them.
 """
 import math
 
@@ -24,6 +27,8 @@ WORKLOADS = {
     "headline": dict(shape=(2, 16, 128, 128, 128), k=7, dtype="float32"),
     "bf16": dict(shape=(2, 16, 128, 128, 128), k=5, dtype="bfloat16"),
     "large": dict(shape=(2, 16, 256, 256, 256), k=7, dtype="float32"),
+    "feat16": dict(shape=(1, 256, 16, 16, 16), k=7, dtype="float32"),
+    "feat64": dict(shape=(2, 64, 64, 64, 64), k=7, dtype="float32"),
 }
 
 
@@ -69,6 +74,9 @@ def make_inputs(name, shape=None):
         p = 0.8 * t + 0.6 * torch.randn(shape, generator=_gen(1))
         if name == "bf16":
             t, p = t.to(torch.bfloat16), p.to(torch.bfloat16)
+    elif name in ("feat16", "feat64"):
+        p = torch.randn(shape, generator=_gen(0))
+        t = torch.randn(shape, generator=_gen(1))
     else:
         raise KeyError(name)
     return p.contiguous(), t.contiguous()

@@ -98,8 +98,9 @@ def test_workspace_bytes():
 def test_lds_bytes():
     lib = _lib.load()
     sizes = [lib.fl_lds_bytes(k, _lib.FL_F32) for k in (3, 5, 7, 9)]
-    # k = 9 runs on a 32 x 24 tile, so it needs less than k = 7 on 32 x 32
-    assert all(0 < b <= 160 * 1024 for b in sizes) and sizes[:3] == sorted(sizes[:3])
+    # the larger of the two kernels: the small-volume kernel's eight 16^3 float fields and 16
+    # float64 partials (131200 B) exceed the plane-marching kernel's at every k
+    assert sizes == [8 * 16 ** 3 * 4 + 16 * 8] * 4 and all(b <= 160 * 1024 for b in sizes)
     assert lib.fl_lds_bytes(7, _lib.FL_BF16) == sizes[2]
     assert lib.fl_lds_bytes(8, _lib.FL_F32) == 0 and lib.fl_lds_bytes(7, 5) == 0
 
