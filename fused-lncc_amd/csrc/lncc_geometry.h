@@ -123,6 +123,21 @@ struct Geo {
     static_assert(LDS_FLOATS * 4 <= 160 * 1024, "LDS");
 };
 
+// ---- the small-volume kernel (lncc_small.hip): one workgroup of kSmallLanes lanes per volume
+// whose D, H, W are all at most kSmallEdge, the volume zero-padded to kSmallEdge^3 in LDS. Lanes
+// form four quarters q (whole waves) of 16 x 16; a quarter owns positions 4q..4q+3 of a line and
+// reads positions 4q-h+i, i < 4+2h, of it (zero outside [0, 16)).
+constexpr int kSmallEdge = 16;
+constexpr int kSmallLanes = 1024;
+// LDS offset of (z, y, x) in one 16^3 field: each z plane's 16-float rows rotated by z, so that the
+// 64 lanes of a wave, four consecutive y (or z) of one 16-wide x row each, hit 64 distinct banks.
+FL_HD constexpr int small_lds(int z, int y, int x) { return (z << 8) | (((y + z) & 15) << 4) | x; }
+// The code class of lane quarter q: 0 (q = 0: reads below position 0 are zeros), 3 (q = 3: reads
+// past position 15 are zeros), 1 (q = 1, 2: every read is inside the line, for h <= 4).
+FL_HD constexpr int small_class(int q) { return q == 0 ? 0 : q == 3 ? 3 : 1; }
+// Whether read i (position 4q-h+i) of a quarter of class qc is a compile-time zero.
+FL_HD constexpr bool small_skip(int qc, int h, int i) { return (qc == 0 && i < h) || (qc == 3 && i >= 4 + h); }
+
 // Lane order for work over n_rows rows of LEN (>= 32) positions: indices [0, 32 n_rows) take
 // positions 0..31 of one row per 32 consecutive lanes, so that each half-wave stores into a
 // single destination row (consecutive LDS banks, no conflicts); the remaining indices take

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "lncc_geometry.h"
+
 namespace fl {
 
 enum Mode { MODE_LOSS = 0, MODE_GRAD = 1, MODE_MAPS = 2 };
@@ -39,10 +41,9 @@ hipError_t launch_fused_h2(int mode, bool bf16, const FusedArgs& a, uint32_t nbl
 hipError_t launch_fused_h3(int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
 hipError_t launch_fused_h4(int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
 
-// The small-volume kernel (lncc_small.hip): volumes whose D, H and W are all at most kSmallEdge,
-// one workgroup of kSmallLanes lanes per volume (FusedArgs' tile and chunk fields unused).
-constexpr int kSmallEdge = 16;
-constexpr int kSmallLanes = 1024;
+// The small-volume kernel (lncc_small.hip): volumes whose D, H and W are all at most kSmallEdge
+// (lncc_geometry.h), one workgroup of kSmallLanes lanes per volume (FusedArgs' tile and chunk
+// fields unused).
 hipError_t launch_small(int halo, int mode, bool bf16, const FusedArgs& a, uint32_t nblocks, hipStream_t st);
 
 // box3d (nfields = 1, fp32 out) and the reference backward combine (nfields = 3): workgroups of

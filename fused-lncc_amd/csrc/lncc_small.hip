@@ -36,10 +36,8 @@ constexpr int SQ = 4;              // outputs per lane along its line
 constexpr int SF = kSmallEdge * kSmallEdge * kSmallEdge;   // floats per field (16^3)
 static_assert(SNT == 4 * kSmallEdge * kSmallEdge && kSmallEdge == 4 * SQ, "lane quarters");
 
-// LDS offset of (z, y, x) in one field. Each z plane's rows are rotated by z, so that the 64 lanes
-// of a wave, which cover four consecutive y (phases A, D) or four consecutive z (B, C) of one
-// 16-wide x row each, always hit four different 16-float rows and thus 64 different banks.
-__device__ __forceinline__ int sidx(int z, int y, int x) { return (z << 8) | (((y + z) & 15) << 4) | x; }
+// LDS offset of (z, y, x) in one field (rows rotated by z: conflict-free for every phase's waves)
+__device__ __forceinline__ int sidx(int z, int y, int x) { return small_lds(z, y, x); }
 
 template <int D>
 __device__ __forceinline__ float dpp_from_below(float v) {   // lane x gets x - D of its row, 0 past the edge
@@ -68,10 +66,7 @@ template <int HH, int QC, class At>
 __device__ __forceinline__ void line4(int q, At at, float (&out)[SQ]) {
     float v[SQ + 2 * HH];
 #pragma unroll
-    for (int i = 0; i < SQ + 2 * HH; ++i) {
-        const bool outside = (QC == 0 && i < HH) || (QC == 3 && i >= SQ + HH);
-        v[i] = outside ? 0.f : at(4 * q - HH + i);
-    }
+    for (int i = 0; i < SQ + 2 * HH; ++i) v[i] = small_skip(QC, HH, i) ? 0.f : at(4 * q - HH + i);
     box_sums<HH, SQ>(v, out);
 }
 
@@ -136,9 +131,10 @@ __global__ __launch_bounds__(SNT, 1) void lncc_small_kernel(FusedArgs a) {
 #pragma unroll
             for (int f = 0; f < NF; ++f) line4<HH, QC>(q, [&](int pos) { return at(f, pos); }, out[f]);
         };
-        if (q == 0)
+        const int qc = small_class(q);
+        if (qc == 0)
             run(std::integral_constant<int, 0>{});
-        else if (q == 3)
+        else if (qc == 3)
             run(std::integral_constant<int, 3>{});
         else
             run(std::integral_constant<int, 1>{});
