@@ -1,12 +1,19 @@
 """ctypes binding of libfused_lncc_hip.so (C ABI in include/fused_lncc.h).
 
-Loading fails loudly when the library has not been built: there is no CPU fallback.
+On first use a missing library is built from the package's HIP sources (hipcc, gfx950), as the
+reference compiles its extension on first import (fused_lncc/__init__.py:10-19); set
+FUSED_LNCC_NO_BUILD=1 to turn that off. Loading fails loudly when the library is neither built
+nor buildable: there is no CPU fallback.
 """
 import ctypes
 import os
+import subprocess
+import sys
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libfused_lncc_hip.so")
+_DEFAULT_LIB = LIB_PATH
+_BUILD_SCRIPT = os.path.join(os.path.dirname(_HERE), "build.py")
 
 FL_F32 = 0
 FL_BF16 = 1
@@ -53,10 +60,30 @@ class FusedLNCCError(RuntimeError):
         self.code = code
 
 
+def _build_missing_library():
+    """Build the in-package library with build.py, once per machine: concurrent first uses wait
+    on a lock file, and the one that finds the library built on waking does nothing. Raises
+    ImportError with the compiler's messages when the build fails."""
+    import fcntl
+    with open(LIB_PATH + ".lock", "w") as lock:
+        fcntl.flock(lock, fcntl.LOCK_EX)
+        if os.path.exists(LIB_PATH):
+            return
+        print(f"fused_lncc: {LIB_PATH} is missing; building it (hipcc, gfx950) ...", file=sys.stderr, flush=True)
+        r = subprocess.run([sys.executable, _BUILD_SCRIPT], capture_output=True, text=True)
+        if r.returncode != 0 or not os.path.exists(LIB_PATH):
+            tail = "\n".join((r.stdout + r.stderr).strip().splitlines()[-20:])
+            raise ImportError(f"fused_lncc: building {LIB_PATH} failed:\n{tail}\nThere is no CPU fallback.")
+
+
 def load():
-    """Load the library once (the HIP runtime it links is the one torch already loaded)."""
+    """Load the library once (the HIP runtime it links is the one torch already loaded), building
+    it first when it is missing (module docstring)."""
     global _lib
     if _lib is None:
+        if (not os.path.exists(LIB_PATH) and LIB_PATH == _DEFAULT_LIB and os.path.exists(_BUILD_SCRIPT)
+                and os.environ.get("FUSED_LNCC_NO_BUILD") != "1"):
+            _build_missing_library()
         if not os.path.exists(LIB_PATH):
             raise ImportError(
                 f"fused_lncc: {LIB_PATH} is not built; run `python fused-lncc_amd/build.py` "

@@ -291,3 +291,36 @@ def test_missing_library_fails_loudly():
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
     assert out.returncode == 0, out.stderr
     assert "ImportError:" in out.stdout and "no CPU fallback" in out.stdout
+
+
+def _package_copy(tmp_path):
+    """The package, its build script and HIP sources, and the C-ABI header they include, copied
+    without any built file."""
+    import shutil
+    src = os.path.join(ROOT, "fused-lncc_amd")
+    dst = tmp_path / "fused-lncc_amd"
+    shutil.copytree(src, dst, ignore=shutil.ignore_patterns("_build", "*.so", "*.so.tmp", "*.lock", "__pycache__"))
+    shutil.copytree(os.path.join(ROOT, "include"), tmp_path / "include")
+    return dst
+
+
+def test_first_use_builds_missing_library(tmp_path):
+    """A package without its library builds it on the first call that needs it (as the reference
+    compiles its extension on first import), and the result exports every symbol of the C ABI;
+    with FUSED_LNCC_NO_BUILD=1 the same call fails loudly instead."""
+    import subprocess
+    import sys
+    pkg = _package_copy(tmp_path)
+    code = ("import fused_lncc._lib as L\n"
+            "lib = L.load()\n"
+            "print('loaded', L.LIB_PATH, all(hasattr(lib, n) for n in L.SIGNATURES))\n")
+    env = dict(os.environ, PYTHONPATH=str(pkg))
+    env.pop("FUSED_LNCC_NO_BUILD", None)
+    off = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                         env=dict(env, FUSED_LNCC_NO_BUILD="1"), timeout=300)
+    assert off.returncode != 0 and "no CPU fallback" in off.stderr
+    assert not (pkg / "fused_lncc" / "libfused_lncc_hip.so").exists()
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=900)
+    assert out.returncode == 0, out.stderr[-3000:]
+    assert "building it" in out.stderr
+    assert out.stdout.strip() == f"loaded {pkg / 'fused_lncc' / 'libfused_lncc_hip.so'} True"
