@@ -350,8 +350,26 @@ int fl_lncc_loss_grad_pt(const void* pred, const void* target, int dtype, int64_
     if (rc) return rc;
     if (!pred || !target || !loss || !grad_pred || !grad_target || !workspace)
         return fail(FL_E_NULL, "fl_lncc_loss_grad_pt: NULL pointer argument");
-    // the pred pass with the loss, then the same kernel with pred and target swapped (the loss is
-    // symmetric in its inputs); the second pass's partials are not reduced
+    const int halo = kernel_size / 2;
+    Plan p;
+    rc = planned(B, D, H, W, halo, p, "fl_lncc_loss_grad_pt");
+    if (rc) return rc;
+    if (!p.small && fl::dual_supported(halo)) {
+        // one launch of the plane-marching kernel for both gradients
+        if (workspace_bytes < (size_t)p.nblocks * sizeof(double))
+            return fail(FL_E_WORKSPACE, "fl_lncc_loss_grad_pt: workspace needs " +
+                                            std::to_string((size_t)p.nblocks * sizeof(double)) + " bytes");
+        fl::FusedArgs a = fused_args(pred, target, B, D, H, W, kernel_size, smooth_dr, p);
+        a.grad = grad_pred;
+        a.grad_t = grad_target;
+        a.partials = static_cast<double*>(workspace);
+        hipError_t e = launch_fused(halo, fl::MODE_DUAL, dtype == FL_BF16, a, p, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_fail(e, "fl_lncc_loss_grad_pt: fused kernel launch");
+        return fl_lncc_finalize(workspace, B, D, H, W, kernel_size, loss, stream);
+    }
+    // small volumes and k = 9: the pred pass with the loss, then the same kernel with pred and
+    // target swapped (the loss is symmetric in its inputs); the second pass's partials are not
+    // reduced
     rc = fl_lncc_loss_grad(pred, target, dtype, B, D, H, W, kernel_size, smooth_dr, loss, grad_pred, workspace,
                            workspace_bytes, stream);
     if (rc) return rc;

@@ -46,6 +46,12 @@
 // division by dr^2 blows up). With r = 1/(VP VT), c = X r, u = c VT, w = St - Sp u it carries
 //   alpha = c w, beta = c u, gamma = c   (A = -2 alpha, Bc = -n beta, Cc = 2 n gamma)
 // so that grad = (2n/M) (box(alpha)/n + p box(beta) - t box(gamma)).
+// Both gradients (MODE_DUAL): the loss is symmetric in p and t, and with u' = c VP, w' = Sp - St u'
+// the target's coefficients are alpha' = c w', beta' = c u' and gamma' = c = gamma, so that
+// grad_t = (2n/M) (box(alpha')/n + t box(beta') - p box(gamma)): five adjoint fields through the
+// adjoint passes instead of three, each formed by the same operations on the same values as in a
+// pred-gradient pass over the swapped inputs, so both gradients equal those of two such passes bit
+// for bit.
 // Range: VP VT = n^2 vp vt would overflow n^2 times earlier than the reference's vp vt (at a
 // local standard deviation ~20x smaller at k = 7). The kernel therefore forms VT s instead of VT,
 // with s = 2^-E the power of two just below 1/n^2, so that r and c carry a factor 1/s; ncc is
@@ -115,8 +121,10 @@ __device__ __forceinline__ void lds_store4(float* __restrict__ dst, float x, flo
 
 template <int HH, bool BF16, int MODE>
 __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) {
-    constexpr bool ADJ = (MODE == MODE_GRAD);
-    using G = Geo<HH>;
+    constexpr bool DUAL = (MODE == MODE_DUAL);
+    constexpr bool ADJ = (MODE == MODE_GRAD) || DUAL;
+    constexpr int NADJ = DUAL ? 5 : 3;   // adjoint fields
+    using G = Geo<HH, NADJ>;
     constexpr int K = G::K;
     constexpr int ELEM = BF16 ? 2 : 4;
     constexpr int J = G::J;
@@ -126,9 +134,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // alias the writes of another and can overlap them
     __shared__ __align__(16) float Zs[5 * G::ZP + G::PAD];
     __shared__ __align__(16) float Xs[5 * G::XP + G::PAD];
-    __shared__ __align__(16) float Gs[ADJ ? 3 * G::GP + G::PAD : 4];
-    __shared__ __align__(16) float GXs[ADJ ? 3 * G::GXP + G::PAD : 4];
-    __shared__ __align__(16) float GY[ADJ ? 3 * G::GYP : 2];
+    __shared__ __align__(16) float Gs[ADJ ? NADJ * G::GP + G::PAD : 4];
+    __shared__ __align__(16) float GXs[ADJ ? NADJ * G::GXP + G::PAD : 4];
+    __shared__ __align__(16) float GY[ADJ ? NADJ * G::GYP : 2];
     __shared__ double red[NT / 64];
 
     const int tid = threadIdx.x;
@@ -157,6 +165,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     const char* pvol = (const char*)a.pred + b * D * HW * ELEM;
     const char* tvol = (const char*)a.target + b * D * HW * ELEM;
     char* const gvol = ADJ ? (char*)a.grad + b * D * HW * ELEM : nullptr;
+    char* const gtvol = DUAL ? (char*)a.grad_t + b * D * HW * ELEM : nullptr;
 
     // ---- F: per-lane input columns
     uint32_t voff[J];
@@ -174,7 +183,8 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     if constexpr (G::FPAIR) zaddr[1] = zaddr[0] + NT;  // a lane without a second column writes padding
     // Y items on lanes [0, YITEMS) (y-sums in P0, ncc arithmetic in P1), X and AYs units in P1,
     // AX units in P0 (lncc_geometry.h); offsets into the source and destination buffers
-    // (a lane has at most one P1 unit, X or AYs, so the two share one pair of offsets)
+    // (a lane has at most one unit of X and AYs, so the two share one pair of offsets; with five
+    // adjoint fields the AYs units sit on Y lanes)
     int u_src, u_dst, a_src, a_dst, b_src, b_dst;
     const bool has_x = x_unit<G>(tid, u_src, u_dst);
     const bool has_a = ax_unit<G>(tid, a_src, a_dst) && ADJ;
@@ -188,8 +198,8 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // the Y item's offsets into Xs and Gs. At k = 7 they take the registers of the X / AYs unit
     // offsets (a Y lane has no such unit), which with three of Y's rows in flight across F is
     // what keeps the kernel within 128 registers; at the other k separate registers measured
-    // faster (k = 9: 1%).
-    constexpr bool Y_SHARE = HH == 3;
+    // faster (k = 9: 1%). With both gradients the Y lanes carry AYs units, whose offsets those are.
+    constexpr bool Y_SHARE = HH == 3 && !DUAL;
     int y_xs = 0, y_gs0 = 0;
     if (has_y) {
         y_item<G>(tid, y_seg, y_ax);
@@ -255,11 +265,11 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             tnext[j] = load_elem<BF16>(rt, voff[j]);
         }
     }
-    // AZ state: the ring of the last k planes' xy-sums of alpha, beta, gamma and their prefix sums
+    // AZ state: the ring of the last k planes' xy-sums of the adjoint fields and their prefix sums
     // over the current block
-    float gring[3][K], gpre[3];
+    float gring[NADJ][K], gpre[NADJ];
 #pragma unroll
-    for (int c = 0; c < 3; ++c) {
+    for (int c = 0; c < NADJ; ++c) {
         gpre[c] = 0.f;
 #pragma unroll
         for (int r = 0; r < K; ++r) gring[c][r] = 0.f;
@@ -274,7 +284,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     // zero-sized resource (its address is never dereferenced).
     const uint64_t PB = (uint64_t)HW * ELEM;
     const uint64_t pva = (uint64_t)(uintptr_t)pvol, tva = (uint64_t)(uintptr_t)tvol;
-    const uint64_t gva = (uint64_t)(uintptr_t)gvol;
+    const uint64_t gva = (uint64_t)(uintptr_t)gvol, gtva = (uint64_t)(uintptr_t)gtvol;
     uint64_t zoff = (uint64_t)zlo * PB;
     const int zn_hi = min(zhi, D);                 // F: new plane zi+1 valid while zi+1 < zn_hi
     constexpr int ZO = 3 + 2 * HH;                 // AZ: output plane zi-ZO
@@ -293,7 +303,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     auto y_math = [&](const float (&S)[5][G::SY], int zcY) __attribute__((always_inline)) {
         const bool count = zcY >= z0 && zcY < z1;
         float lsum = -0.f;  // -0 + x == x for every x, so the first add folds away
-        float adj[3][G::SY];  // alpha, beta, gamma of the segment's outputs
+        float adj[NADJ][G::SY];  // alpha, beta, gamma (and alpha', beta') of the segment's outputs
 #pragma unroll
         for (int i = 0; i < G::SY; ++i) {
             const int ay = y_start + i;
@@ -315,14 +325,18 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 const float crm = live ? cr : 0.f;
                 const float uu = crm * VT;
                 const float w = fmaf(-Sp, uu, St);
-                if constexpr (G::ASWAP) {
-                    adj[0][i] = crm * w;
-                    adj[1][i] = crm * uu;
-                    adj[2][i] = crm;
-                } else {
-                    Gs[y_go + i * G::GST] = crm * w;
-                    Gs[y_go + G::GP + i * G::GST] = crm * uu;
-                    Gs[y_go + 2 * G::GP + i * G::GST] = crm;
+                adj[0][i] = crm * w;
+                adj[1][i] = crm * uu;
+                adj[2][i] = crm;
+                if constexpr (DUAL) {
+                    // the target's: u' = (c/s)(VP s), w' = Sp - St u' (the swapped pass's uu, w)
+                    const float uu2 = crm * (VP * VS);
+                    adj[3][i] = crm * fmaf(-St, uu2, Sp);
+                    adj[4][i] = crm * uu2;
+                }
+                if constexpr (!G::ASWAP) {
+#pragma unroll
+                    for (int c = 0; c < NADJ; ++c) Gs[y_go + c * G::GP + i * G::GST] = adj[c][i];
                 }
             }
             if constexpr (MODE == MODE_MAPS) {
@@ -343,7 +357,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
         if constexpr (ADJ && G::ASWAP) {  // Gs rows along y: one float4 per field
             static_assert(G::SY == 4, "float4 rows");
 #pragma unroll
-            for (int c = 0; c < 3; ++c)
+            for (int c = 0; c < NADJ; ++c)
                 lds_store4(Gs + y_go + c * G::GP, adj[c][0], adj[c][1], adj[c][2], adj[c][3]);
         }
         loss_acc += (double)lsum;
@@ -405,17 +419,24 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     //    before F measured 1% slower than after it.)
     //  * P1: the Y lanes turn their box sums into ncc and the adjoint coefficients (arithmetic
     //    only, no LDS reads: it keeps the SIMDs busy while the rows of the X and AYs units, on the
-    //    other waves, arrive), then the X and AYs units.
-    constexpr int Y_EARLY = HH <= 2 ? 5 : HH == 3 ? (BF16 ? 2 : 3) : 0;   // Y rows read before F
+    //    other waves, arrive), then the X and AYs units (with both gradients, at k >= 5, also on
+    //    the first Y lanes: units that do not fit after the X units, 2-7% faster than all AYs
+    //    units on Y lanes).
+    //  * Both gradients (five adjoint fields, ten more ring registers per lane at k = 7): fewer
+    //    early rows, all five at k = 3, two (bf16) or none (fp32) at k = 5, one at k = 7 (more
+    //    spill; the counts are the fastest measured: k = 5 fp32 with none 1.2% faster than with
+    //    two, bf16 with two 0.4% faster than with none), and no AX row before F.
+    constexpr int Y_EARLY = DUAL ? (HH <= 1 ? 5 : HH == 2 ? (BF16 ? 2 : 0) : HH == 3 ? 1 : 0)
+                                 : HH <= 2 ? 5 : HH == 3 ? (BF16 ? 2 : 3) : 0;   // Y rows read before F
     constexpr bool F_STORE_AT_ONCE = Y_EARLY < 5;
     // Y_MID of Y's rows are read between F's two columns, after the box sums of the early rows
     // (whose registers they take); the rest after F. k = 9: one row (0.6-1% faster than none).
     // k = 7: one row measured 0.7% faster at (2,16,128^3) but 1.3% slower at (2,16,256^3), whose
     // re-reads of the output planes then missed the L2 more often (HBM reads 1.05x -> up to 1.46x
     // the inputs, growing from launch to launch); none.
-    constexpr int Y_MID = HH == 4 && J == 2 ? 1 : 0;
+    constexpr int Y_MID = HH == 4 && J == 2 && !DUAL ? 1 : 0;
     static_assert(Y_EARLY + Y_MID <= 5, "Y rows");
-    constexpr bool AX_EARLY = HH <= 2;                        // the AX row read before F
+    constexpr bool AX_EARLY = HH <= 2 && !DUAL;               // the AX row read before F
     constexpr int NY = G::SY + 2 * HH, NA = G::SA + 2 * HH, NX = G::SX + 2 * HH, NB = G::SB + 2 * HH;
     // P0's early reads (Y's first rows or the AX row) share one register array: the two kinds of
     // lane sit on different waves
@@ -437,10 +458,10 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
             // ============================ phase P0 ============================
             // AZ(zi-3) reads, Y(zi-1) y-sums, AX(zi-2), F(zi), AZ(zi-3)
             // AZ's xy-sums: read first, except at k = 9, where they would be held across F
-            float ys[3];
+            float ys[NADJ];
             auto az_read = [&]() __attribute__((always_inline)) {
 #pragma unroll
-                for (int c = 0; c < 3; ++c) {
+                for (int c = 0; c < NADJ; ++c) {
                     // read whatever actA says (the value is dropped when it is false), so that the
                     // three reads pair up
                     const float gy = GY[c * G::GYP + z_oy * G::GYS + z_ox];
@@ -527,9 +548,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 // (lanes without an output column run on a clamped one and store out of range,
                 // i.e. nothing)
                 constexpr int r = decltype(rc)::value;
-                float gw[3];
+                float gw[NADJ];
 #pragma unroll
-                for (int c = 0; c < 3; ++c) gw[c] = zstep1<K, r, A_CHAIN>(ys[c], gpre[c], gring[c]);
+                for (int c = 0; c < NADJ; ++c) gw[c] = zstep1<K, r, A_CHAIN>(ys[c], gpre[c], gring[c]);
                 const int zo = zi - ZO;
                 const float g = a.gscale * fmaf(inv_n, gw[0], fmaf(pz, gw[1], -tzz * gw[2]));   // gscale holds s
                 // Non-temporal: the gradient is never read back, and this re-read of p,t is the
@@ -541,6 +562,10 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
                 // those stores keep the default policy, so that the L2 merges the two halves into
                 // one write.
                 store_elem_buf<BF16, BF16 ? 0 : kNT>(rsrc_at(gva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, g);
+                if constexpr (DUAL) {
+                    const float gt = a.gscale * fmaf(inv_n, gw[3], fmaf(tzz, gw[4], -pz * gw[2]));
+                    store_elem_buf<BF16, BF16 ? 0 : kNT>(rsrc_at(gtva + zoff - ZO * PB, plane_bytes, zo >= z0 && zo < z1), z_voff, gt);
+                }
                 // prefetch p,t at the next step's output plane; issued after this step's use, so
                 // one register each suffices and no copy has to wait for the load
                 const bool oko = zo + 1 >= z0 && zo + 1 < z1;
@@ -605,6 +630,12 @@ hipError_t launch_fused(int mode, bool bf16, const FusedArgs& a, uint32_t nblock
         if (bf16) FL_LAUNCH(true, MODE_GRAD); else FL_LAUNCH(false, MODE_GRAD);
     } else if (mode == MODE_MAPS) {
         if (bf16) FL_LAUNCH(true, MODE_MAPS); else FL_LAUNCH(false, MODE_MAPS);
+    } else if (mode == MODE_DUAL) {
+        if constexpr (dual_supported(HH)) {
+            if (bf16) FL_LAUNCH(true, MODE_DUAL); else FL_LAUNCH(false, MODE_DUAL);
+        } else {
+            return hipErrorInvalidValue;
+        }
     } else {
         return hipErrorInvalidValue;
     }

@@ -51,10 +51,13 @@ FL_HD constexpr int row_read(int n) { return n % 4 == 3 ? rup4(n) : n; }
 // The box-sum passes work on segments of S consecutive outputs. The X and Y passes round their
 // output range up to whole segments: the extra outputs read row padding and land in padding rows
 // of the destination that no later pass reads (and that the loss never counts), so no lane needs
-// a per-output store mask. Three adjoint fields (alpha, beta, gamma) go from Y to AZ.
-template <int H>
+// a per-output store mask. NA adjoint fields go from Y to AZ: three (alpha, beta, gamma) for the
+// pred gradient, five for both gradients (the target's alpha' and beta' besides; its gamma' is
+// gamma).
+template <int H, int NA = 3>
 struct Geo {
-    static constexpr int HALO = H, NADJ = 3;
+    static_assert(NA == 3 || NA == 5, "adjoint fields");
+    static constexpr int HALO = H, NADJ = NA;
     static constexpr int K = 2 * H + 1;
     static constexpr int TY = tile_rows(H);
     static constexpr int IX = TX + 4 * H, IY = TY + 4 * H;
@@ -85,14 +88,20 @@ struct Geo {
     //   P1  Y's ncc arithmetic on the same lanes; X units on [XL0, XL0 + UX); AYs units on
     //       [BL0, BL0 + UB)
     // (F and AZ run on every lane in P0.) Waves sit on the CU's 4 SIMDs round-robin (wave w on
-    // SIMD w % 4): the AX waves go to the SIMDs with fewer Y waves, which evens out P0.
-    static constexpr int UX = 5 * XITEMS, UA = 3 * AITEMS, UB = 3 * BITEMS;
+    // SIMD w % 4): with three adjoint fields the AX waves go to the SIMDs with fewer Y waves, which
+    // evens out P0. With five the AX units run on the waves after Y's, and the AYs units that do
+    // not fit on the lanes after the X units (BOWN of them do) run on the first Y lanes, after Y's
+    // ncc arithmetic (which reads no LDS row).
+    static constexpr int UX = 5 * XITEMS, UA = NA * AITEMS, UB = NA * BITEMS;
     static constexpr int NYW = cdiv(YITEMS, 64), XL0 = 64 * NYW, BL0 = rup64(XL0 + UX), NAW = cdiv(UA, 64);
-    // Y items, X units and AYs units on disjoint lanes (the kernel keeps a Y item's offsets in the
-    // registers of the X / AYs unit offsets at k = 7)
-    static_assert(XL0 >= YITEMS && BL0 >= XL0 + UX, "lane kinds");
-    static_assert(BL0 + UB <= NT && NAW <= 4 && (NYW == 5 || NYW == 6) && BPOS == 32 && TX == 32 &&
-                      NIN <= 2 * NT && TY <= TY_MAX,
+    static constexpr int BOWN = UB < NT - BL0 ? UB : NT - BL0;
+    static constexpr bool B_ON_Y = UB > BOWN;
+    // Y items and X units on disjoint lanes, AYs units on lanes of their own or on Y lanes (the
+    // kernel keeps a Y item's offsets in the registers of the X / AYs unit offsets at k = 7 with
+    // three adjoint fields)
+    static_assert(XL0 >= YITEMS && BL0 >= XL0 + UX && UB - BOWN <= YITEMS && (NA > 3 || !B_ON_Y), "lane kinds");
+    static_assert(BL0 <= NT && (NA > 3 ? NYW + NAW <= NT / 64 : NAW <= 4) && (NYW == 5 || NYW == 6) &&
+                      BPOS == 32 && TX == 32 && NIN <= 2 * NT && TY <= TY_MAX,
                   "lanes");
     // every segment starts on a 16-byte boundary (rows are read as float4)
     static_assert(XR >= AX && ASEG * SA == (ASWAP ? TY : TX) && BSEG * SB == (ASWAP ? TX : TY) && SX % 4 == 0 && SY % 4 == 0 &&
@@ -119,7 +128,7 @@ struct Geo {
     static_assert(SX + row_read(SX + 2 * H) <= ZS + PAD && YR - SY + row_read(SY + 2 * H) <= XS + PAD &&
                       (ASEG - 1) * SA + row_read(SA + 2 * H) <= GS + PAD && (BSEG - 1) * SB + row_read(SB + 2 * H) <= GXS + PAD,
                   "row reads");
-    static constexpr int LDS_FLOATS = 5 * (ZP + XP) + 3 * (GP + GXP + GYP) + 4 * PAD;
+    static constexpr int LDS_FLOATS = 5 * (ZP + XP) + NA * (GP + GXP + GYP) + 4 * PAD;
     static_assert(LDS_FLOATS * 4 <= 160 * 1024, "LDS");
 };
 
@@ -187,12 +196,13 @@ FL_HD inline bool x_unit(int tid, int& src, int& dst) {
     return true;
 }
 
-// The waves of the AX units: those of the SIMDs with fewer Y waves first (6 Y waves: SIMDs 0
-// and 1 carry two each; 5: SIMD 0 does).
+// The waves of the AX units. Three adjoint fields: those of the SIMDs with fewer Y waves first
+// (6 Y waves: SIMDs 0 and 1 carry two each; 5: SIMD 0 does). Five: the waves after Y's.
 template <class G>
 FL_HD constexpr int ax_wave(int slot) {
-    return G::NYW == 6 ? (slot == 0 ? 6 : slot == 1 ? 7 : slot == 2 ? 10 : 11)
-                       : (slot == 0 ? 5 : slot == 1 ? 6 : slot == 2 ? 7 : 9);
+    return G::NADJ > 3 ? G::NYW + slot
+                       : G::NYW == 6 ? (slot == 0 ? 6 : slot == 1 ? 7 : slot == 2 ? 10 : 11)
+                                     : (slot == 0 ? 5 : slot == 1 ? 6 : slot == 2 ? 7 : 9);
 }
 
 // AX unit of lane tid (phase P0): sums of one adjoint field over one segment of position pos
@@ -243,8 +253,9 @@ template <class G>
 FL_HD inline bool ays_unit(int tid, int& src, int& dst) {
     src = 0;
     dst = 0;
-    const int u = tid - G::BL0;
-    if (u < 0 || u >= G::UB) return false;
+    // units [0, BOWN) on lanes BL0.., the rest on lanes 0..
+    const int u = tid >= G::BL0 ? tid - G::BL0 : G::BOWN + tid;
+    if (u >= G::UB) return false;
     const int row = u >> 5, pos = u & 31;  // rows (c, seg) of BPOS = 32 positions
     const int c = row / G::BSEG, start = (row % G::BSEG) * G::SB;
     src = c * G::GXP + pos * G::GXS + start;

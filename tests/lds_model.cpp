@@ -1,5 +1,6 @@
 // Host-side model of the LDS accesses of the fused LNCC kernel (lncc_fused_kernel.h): for every
-// halo h = 1..4 (tile 32 x 32, and 32 x 24 at h = 4) it enumerates the LDS reads and writes of every lane in every
+// halo h = 1..4 (tile 32 x 32, and 32 x 24 at h = 4), with three adjoint fields (pred gradient)
+// and, for h <= 3, five (both gradients), it enumerates the LDS reads and writes of every lane in every
 // stage from the same lane maps the kernel uses (lncc_geometry.h) and checks
 //   bounds    every access lies inside its __shared__ array (spare floats included);
 //   races     within a phase no address is written twice, and no array written in a phase is read
@@ -66,13 +67,13 @@ struct Model {
     }
 };
 
-template <int H>
+template <int H, int NADJ = 3>
 long check(int plant) {
-    using G = fl::Geo<H>;
+    using G = fl::Geo<H, NADJ>;
     constexpr int NA = G::NADJ;
     Model m;
     m.plant = plant;
-    m.cfg = "h=" + std::to_string(H) + " tile 32x" + std::to_string(G::TY);
+    m.cfg = "h=" + std::to_string(H) + " tile 32x" + std::to_string(G::TY) + " " + std::to_string(NA) + " adjoint fields";
     m.size = {5L * G::ZP + G::PAD, 5L * G::XP + G::PAD, (long)NA * G::GP + G::PAD,
               (long)NA * G::GXP + G::PAD, (long)NA * G::GYP};
     for (int p = 0; p < 2; ++p) {
@@ -122,11 +123,14 @@ long check(int plant) {
             for (int i = 0; i < G::SX; ++i) m.write(1, XS, dst + (long)i * G::XS);
         if (fl::ax_unit<G>(tid, src, dst))
             for (int i = 0; i < G::SA; ++i) m.write(0, GXS, dst + (long)i * G::GXS);
-        // lane kinds: a lane has at most one of Y, X, AYs (P1) and at most one of Y, AX (P0)
+        // lane kinds: a lane has at most one of Y, X, AYs (P1; with five adjoint fields the AYs
+        // units run on Y lanes after Y's arithmetic, which reads no LDS row) and at most one of
+        // Y, AX (P0)
         int s2, d2;
-        const int p1 = (tid < G::YITEMS) + fl::x_unit<G>(tid, s2, d2) + fl::ays_unit<G>(tid, s2, d2);
-        const int p0 = (tid < G::YITEMS) + fl::ax_unit<G>(tid, s2, d2);
-        if (p1 > 1 || p0 > 1) m.fail("lane " + std::to_string(tid) + " has two units in one phase");
+        const bool y = tid < G::YITEMS, x = fl::x_unit<G>(tid, s2, d2), b = fl::ays_unit<G>(tid, s2, d2);
+        const bool two_p1 = (x && (y || b)) || (y && b && !G::B_ON_Y);
+        const int p0 = y + fl::ax_unit<G>(tid, s2, d2);
+        if (two_p1 || p0 > 1) m.fail("lane " + std::to_string(tid) + " has two units in one phase");
     }
     // ---- races: one write per address per phase
     for (int p = 0; p < 2; ++p)
@@ -217,6 +221,9 @@ int main(int argc, char** argv) {
     f += check<2>(plant);
     f += check<3>(plant);
     f += check<4>(plant);
+    f += check<1, 5>(plant);
+    f += check<2, 5>(plant);
+    f += check<3, 5>(plant);
     std::printf("%s\n", f ? "FAILED" : "all ok");
     return f ? 1 : 0;
 }

@@ -1,7 +1,8 @@
 """The fused kernel's LDS accesses, checked on the host (tests/lds_model.cpp): bounds, write
 collisions within a phase, arrays read and written in one phase, and that every read feeding a
-used output reads what the producing stage wrote, for every kernel size, from the lane maps the
-kernel itself uses (fused-lncc_amd/csrc/lncc_geometry.h).
+used output reads what the producing stage wrote, for every kernel size and both adjoint layouts
+(three fields for the pred gradient, five for both gradients), from the lane maps the kernel
+itself uses (fused-lncc_amd/csrc/lncc_geometry.h).
 
 This is the stand-in for the reference's compute-sanitizer workloads (tests/_sanitize*.py): GPU
 address sanitizers are not available for LDS and ROCm has no LDS race checker. Each planted
@@ -33,7 +34,9 @@ def test_kernel_lane_maps_pass(model):
     assert r.returncode == 0, r.stdout + r.stderr
     lines = r.stdout.strip().splitlines()
     assert lines[-1] == "all ok"
-    assert len([ln for ln in lines if ln.endswith(", ok")]) == 4   # h = 1..4
+    # h = 1..4 with three adjoint fields, h = 1..3 with five (both gradients)
+    assert len([ln for ln in lines if ln.endswith(", ok")]) == 7
+    assert len([ln for ln in lines if "5 adjoint fields" in ln]) == 3
 
 
 @pytest.mark.parametrize("plant,kind", [(1, "used read of unwritten Zs"), (2, "Y window past the row read"),
