@@ -157,11 +157,18 @@ def main():
     nbytes = lib.fl_workspace_bytes(B, D, H, W, k)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     grad = torch.empty_like(p)
+    grad_t = torch.empty_like(t) if a.target_grad else None
+    loss_buf = torch.empty(1, device=dev)
     stream = torch.cuda.current_stream(dev)
 
     def kernel():
-        _lib.check(lib.fl_lncc_fused_partials(p.data_ptr(), t.data_ptr(), code, B, D, H, W, k, 1e-5,
-                                              grad.data_ptr(), ws.data_ptr(), nbytes, stream.cuda_stream))
+        if a.target_grad:   # both gradients: the one fused launch (k <= 7) and the loss finalize
+            _lib.check(lib.fl_lncc_loss_grad_pt(p.data_ptr(), t.data_ptr(), code, B, D, H, W, k, 1e-5,
+                                                loss_buf.data_ptr(), grad.data_ptr(), grad_t.data_ptr(),
+                                                ws.data_ptr(), nbytes, stream.cuda_stream))
+        else:
+            _lib.check(lib.fl_lncc_fused_partials(p.data_ptr(), t.data_ptr(), code, B, D, H, W, k, 1e-5,
+                                                  grad.data_ptr(), ws.data_ptr(), nbytes, stream.cuda_stream))
 
     # Clock settle. The first step pays one-time host costs (torch loads the code of its fill
     # kernel, the autograd engine starts its device thread: ~25 ms with the GPU idle), so it runs
@@ -194,7 +201,7 @@ def main():
     torch.cuda.synchronize()
     kms = [kev[2 * i].elapsed_time(kev[2 * i + 1]) for i in range(a.kernel_reps)]
     kernel_ms = sum(kms) / len(kms)
-    del grad, ws
+    del grad, grad_t, ws
 
     for _ in range(a.warmup):
         step()
@@ -210,13 +217,13 @@ def main():
     ms_per_step = total_ms / a.steps
     median_ms = per[len(per) // 2]
 
-    alg_bytes = V * BYTES_PER_VOXEL[dtname]
-    achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
-    # the step's algorithmic bytes: with the target gradient, one more gradient is written
+    # algorithmic bytes: with the target gradient, one more gradient is written
     step_bpv = BYTES_PER_VOXEL[dtname] + (BYTES_PER_VOXEL[dtname] // 3 if a.target_grad else 0)
     step_bytes = V * step_bpv
+    alg_bytes = step_bytes
+    achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
     traffic = None
-    if os.path.exists(TRAFFIC_FILE):
+    if os.path.exists(TRAFFIC_FILE) and not a.target_grad:
         with open(TRAFFIC_FILE) as f:
             prof = json.load(f)
         if prof.get("workload") == a.workload:
@@ -246,7 +253,8 @@ def main():
                    "input_dtype": dtname, "bytes_per_voxel": step_bpv, "target_grad": a.target_grad},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
-                     "kernel": "lncc_small_kernel" if max(D, H, W) <= 16 else "lncc_fused_kernel",
+                     "kernel": ("lncc_small_kernel" if max(D, H, W) <= 16 else "lncc_fused_kernel") +
+                               (" (both gradients, with the loss finalize)" if a.target_grad else ""),
                      "algorithmic_bytes_per_launch": alg_bytes},
     }
     if not a.no_cpu_baseline:
