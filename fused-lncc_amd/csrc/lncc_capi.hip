@@ -354,7 +354,7 @@ int fl_lncc_loss_grad_pt(const void* pred, const void* target, int dtype, int64_
     Plan p;
     rc = planned(B, D, H, W, halo, p, "fl_lncc_loss_grad_pt");
     if (rc) return rc;
-    if (!p.small && fl::dual_supported(halo)) {
+    if (!p.small) {
         // one launch of the plane-marching kernel for both gradients
         if (workspace_bytes < (size_t)p.nblocks * sizeof(double))
             return fail(FL_E_WORKSPACE, "fl_lncc_loss_grad_pt: workspace needs " +
@@ -367,9 +367,8 @@ int fl_lncc_loss_grad_pt(const void* pred, const void* target, int dtype, int64_
         if (e != hipSuccess) return hip_fail(e, "fl_lncc_loss_grad_pt: fused kernel launch");
         return fl_lncc_finalize(workspace, B, D, H, W, kernel_size, loss, stream);
     }
-    // small volumes and k = 9: the pred pass with the loss, then the same kernel with pred and
-    // target swapped (the loss is symmetric in its inputs); the second pass's partials are not
-    // reduced
+    // small volumes: the pred pass with the loss, then the same kernel with pred and target
+    // swapped (the loss is symmetric in its inputs); the second pass's partials are not reduced
     rc = fl_lncc_loss_grad(pred, target, dtype, B, D, H, W, kernel_size, smooth_dr, loss, grad_pred, workspace,
                            workspace_bytes, stream);
     if (rc) return rc;

@@ -425,7 +425,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     //  * Both gradients (five adjoint fields, ten more ring registers per lane at k = 7): fewer
     //    early rows, all five at k = 3, two (bf16) or none (fp32) at k = 5, one at k = 7 (more
     //    spill; the counts are the fastest measured: k = 5 fp32 with none 1.2% faster than with
-    //    two, bf16 with two 0.4% faster than with none), and no AX row before F.
+    //    two, bf16 with two 0.4% faster than with none), and no AX row before F. At k = 9 the two
+    //    9-plane rings and the five adjoint rings exceed the 128 registers even so: 36-46 spill to
+    //    scratch, and the launch still runs 22-26% faster than two pred-gradient passes.
     constexpr int Y_EARLY = DUAL ? (HH <= 1 ? 5 : HH == 2 ? (BF16 ? 2 : 0) : HH == 3 ? 1 : 0)
                                  : HH <= 2 ? 5 : HH == 3 ? (BF16 ? 2 : 3) : 0;   // Y rows read before F
     constexpr bool F_STORE_AT_ONCE = Y_EARLY < 5;
@@ -631,11 +633,7 @@ hipError_t launch_fused(int mode, bool bf16, const FusedArgs& a, uint32_t nblock
     } else if (mode == MODE_MAPS) {
         if (bf16) FL_LAUNCH(true, MODE_MAPS); else FL_LAUNCH(false, MODE_MAPS);
     } else if (mode == MODE_DUAL) {
-        if constexpr (dual_supported(HH)) {
-            if (bf16) FL_LAUNCH(true, MODE_DUAL); else FL_LAUNCH(false, MODE_DUAL);
-        } else {
-            return hipErrorInvalidValue;
-        }
+        if (bf16) FL_LAUNCH(true, MODE_DUAL); else FL_LAUNCH(false, MODE_DUAL);
     } else {
         return hipErrorInvalidValue;
     }

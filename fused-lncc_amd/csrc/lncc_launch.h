@@ -10,9 +10,6 @@ namespace fl {
 // LOSS: partial sums only; GRAD: and the pred gradient; MAPS: the reference's four maps; DUAL:
 // the partial sums and both gradients (the marching kernel only)
 enum Mode { MODE_LOSS = 0, MODE_GRAD = 1, MODE_MAPS = 2, MODE_DUAL = 3 };
-// MODE_DUAL exists for k <= 7: at k = 9 the register rings of the last 9 planes (p, t of two input
-// columns, five adjoint fields) alone take more than a lane's 128 registers.
-constexpr bool dual_supported(int halo) { return halo <= 3; }
 
 struct FusedArgs {
     const void* pred;

@@ -111,10 +111,10 @@ int fl_lncc_finalize(const void* workspace, int64_t B, int64_t D, int64_t H, int
  * d loss / d target (each in the input dtype, already multiplied by -1/M), all required. No
  * counterpart in the reference, whose gradient goes to pred only (its README.md:116-121); it is
  * the target-side gradient that FireANTs computes for symmetric registration. The loss is symmetric
- * in its two inputs, so the target gradient is the pred gradient with the two swapped. For k <= 7
- * one launch forms both (five adjoint fields instead of three); for k = 9 and for volumes of at
- * most 16^3 it is two passes of the pred-gradient kernel. Either way both gradients equal those of
- * two such passes bit for bit. Same workspace as fl_lncc_loss_grad.
+ * in its two inputs, so the target gradient is the pred gradient with the two swapped. One launch
+ * forms both (five adjoint fields instead of three); for volumes of at most 16^3 it is two passes
+ * of the pred-gradient kernel. Either way both gradients equal those of two such passes bit for
+ * bit. Same workspace as fl_lncc_loss_grad.
  */
 int fl_lncc_loss_grad_pt(const void* pred, const void* target, int dtype, int64_t B, int64_t D, int64_t H,
                          int64_t W, int kernel_size, float smooth_dr, float* loss, void* grad_pred,
