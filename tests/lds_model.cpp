@@ -1,6 +1,6 @@
 // Host-side model of the LDS accesses of the fused LNCC kernel (lncc_fused_kernel.h): for every
 // halo h = 1..4 (tile 32 x 32, and 32 x 24 at h = 4), with three adjoint fields (pred gradient)
-// and, for h <= 3, five (both gradients), it enumerates the LDS reads and writes of every lane in every
+// and with five (both gradients), it enumerates the LDS reads and writes of every lane in every
 // stage from the same lane maps the kernel uses (lncc_geometry.h) and checks
 //   bounds    every access lies inside its __shared__ array (spare floats included);
 //   races     within a phase no address is written twice, and no array written in a phase is read
@@ -224,6 +224,7 @@ int main(int argc, char** argv) {
     f += check<1, 5>(plant);
     f += check<2, 5>(plant);
     f += check<3, 5>(plant);
+    f += check<4, 5>(plant);
     std::printf("%s\n", f ? "FAILED" : "all ok");
     return f ? 1 : 0;
 }

@@ -34,9 +34,9 @@ def test_kernel_lane_maps_pass(model):
     assert r.returncode == 0, r.stdout + r.stderr
     lines = r.stdout.strip().splitlines()
     assert lines[-1] == "all ok"
-    # h = 1..4 with three adjoint fields, h = 1..3 with five (both gradients)
-    assert len([ln for ln in lines if ln.endswith(", ok")]) == 7
-    assert len([ln for ln in lines if "5 adjoint fields" in ln]) == 3
+    # h = 1..4 with three adjoint fields and with five (both gradients)
+    assert len([ln for ln in lines if ln.endswith(", ok")]) == 8
+    assert len([ln for ln in lines if "5 adjoint fields" in ln]) == 4
 
 
 @pytest.mark.parametrize("plant,kind", [(1, "used read of unwritten Zs"), (2, "Y window past the row read"),
