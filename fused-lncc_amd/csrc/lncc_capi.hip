@@ -240,15 +240,16 @@ int fl_validate(int dtype, int kernel_size, int64_t B, int64_t D, int64_t H, int
 size_t fl_lds_bytes(int kernel_size, int dtype) {
     if (check_k(kernel_size) || check_dtype(dtype)) return 0;
     // the static LDS of the gradient kernels: the plane-marching kernel's five z-sum and x-sum
-    // planes, the three adjoint planes at each pass, and the per-wave partials of the loss (the
-    // same for both dtypes); the small-volume kernel's five 16^3 fields (the first three reused for
-    // the adjoints), three more for the adjoint pass, and its per-wave partials. The larger of the two.
+    // planes, the adjoint planes at each pass (five fields for both gradients, the larger), and the
+    // per-wave partials of the loss (the same for both dtypes); the small-volume kernel's five 16^3
+    // fields (the first three reused for the adjoints), three more for the adjoint pass, and its
+    // per-wave partials. The largest of them.
     size_t floats = 0;
     switch (kernel_size / 2) {
-        case 1: floats = fl::Geo<1>::LDS_FLOATS; break;
-        case 2: floats = fl::Geo<2>::LDS_FLOATS; break;
-        case 3: floats = fl::Geo<3>::LDS_FLOATS; break;
-        default: floats = fl::Geo<4>::LDS_FLOATS; break;
+        case 1: floats = fl::Geo<1, 5>::LDS_FLOATS; break;
+        case 2: floats = fl::Geo<2, 5>::LDS_FLOATS; break;
+        case 3: floats = fl::Geo<3, 5>::LDS_FLOATS; break;
+        default: floats = fl::Geo<4, 5>::LDS_FLOATS; break;
     }
     const size_t marching = floats * sizeof(float) + (fl::NT / 64) * sizeof(double);
     const size_t small = (size_t)8 * fl::kSmallEdge * fl::kSmallEdge * fl::kSmallEdge * sizeof(float) +

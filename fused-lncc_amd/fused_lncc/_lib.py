@@ -65,7 +65,13 @@ def _build_missing_library():
     on a lock file, and the one that finds the library built on waking does nothing. Raises
     ImportError with the compiler's messages when the build fails."""
     import fcntl
-    with open(LIB_PATH + ".lock", "w") as lock:
+    try:
+        lock = open(LIB_PATH + ".lock", "w")
+    except OSError as e:   # a read-only install: nothing can be built here
+        raise ImportError(f"fused_lncc: {LIB_PATH} is not built and cannot be built in place ({e}); run "
+                          "`python fused-lncc_amd/build.py` where the package is writable. There is no CPU "
+                          "fallback.") from e
+    with lock:
         fcntl.flock(lock, fcntl.LOCK_EX)
         if os.path.exists(LIB_PATH):
             return

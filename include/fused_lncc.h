@@ -47,8 +47,9 @@ const char* fl_last_error(void);
 int fl_validate(int dtype, int kernel_size, int64_t B, int64_t D, int64_t H, int64_t W);
 
 /*
- * Bytes of LDS one workgroup of the gradient kernels uses for this kernel size, the larger of the
- * plane-marching kernel's and the small-volume kernel's (static; 0 for an invalid k or dtype), for
+ * Bytes of LDS one workgroup of the gradient kernels uses for this kernel size, the largest of the
+ * plane-marching kernel's (with both gradients, its larger form) and the small-volume kernel's
+ * (static; 0 for an invalid k or dtype), for
  * callers that check a device's limit before launching. Replaces the
  * per-call shared-memory cap check of lncc_forward / lncc_backward, fused_lncc/csrc/lncc3d.cu:144-147,
  * 268-270 (MI355X: 160 KB per workgroup; every kernel size fits).

@@ -98,9 +98,12 @@ def test_workspace_bytes():
 def test_lds_bytes():
     lib = _lib.load()
     sizes = [lib.fl_lds_bytes(k, _lib.FL_F32) for k in (3, 5, 7, 9)]
-    # the larger of the two kernels: the small-volume kernel's eight 16^3 float fields and 16
-    # float64 partials (131200 B) exceed the plane-marching kernel's at every k
-    assert sizes == [8 * 16 ** 3 * 4 + 16 * 8] * 4 and all(b <= 160 * 1024 for b in sizes)
+    # the largest of the kernels: at k = 7 the plane-marching kernel with both gradients, whose
+    # 161184 B the profiler reports as its 512-byte-granular allocation of 161280 B; every size
+    # at least the small-volume kernel's eight 16^3 float fields and 16 float64 partials
+    # (131200 B) and within the CU's 160 KiB
+    assert sizes[2] == 161184 and -(-sizes[2] // 512) * 512 == 161280
+    assert all(8 * 16 ** 3 * 4 + 16 * 8 <= b <= 160 * 1024 for b in sizes)
     assert lib.fl_lds_bytes(7, _lib.FL_BF16) == sizes[2]
     assert lib.fl_lds_bytes(8, _lib.FL_F32) == 0 and lib.fl_lds_bytes(7, 5) == 0
 
