@@ -422,9 +422,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void lncc_fused_kernel(FusedArgs a) 
     //    other waves, arrive), then the X and AYs units (with both gradients, at k >= 5, also on
     //    the first Y lanes: units that do not fit after the X units, 2-7% faster than all AYs
     //    units on Y lanes).
-    //  * Both gradients (five adjoint fields, ten more ring registers per lane at k = 7): fewer
-    //    early rows, all five at k = 3, two (bf16) or none (fp32) at k = 5, one at k = 7 (more
-    //    spill; the counts are the fastest measured: k = 5 fp32 with none 1.2% faster than with
+    //  * Both gradients (five adjoint fields, fourteen more ring registers per lane at k = 7):
+    //    fewer early rows, all five at k = 3, two (bf16) or none (fp32) at k = 5, one at k = 7
+    //    (more early rows spill; the counts are the fastest measured: k = 5 fp32 with none 1.2% faster than with
     //    two, bf16 with two 0.4% faster than with none), and no AX row before F. At k = 9 the two
     //    9-plane rings and the five adjoint rings exceed the 128 registers even so: 36-46 spill to
     //    scratch, and the launch still runs 22-26% faster than two pred-gradient passes.
