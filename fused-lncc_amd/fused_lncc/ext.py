@@ -108,8 +108,9 @@ def loss_grad(pf, tf, kernel_size, smooth_dr, need_grad=True):
 
 def loss_grad_pt(pf, tf, kernel_size, smooth_dr):
     """The loss and both gradients (wrt pf and wrt tf, each already multiplied by -1/M) from one
-    call: the pred-gradient kernel, then the same kernel with the inputs swapped (the loss is
-    symmetric in them). Returns (loss, grad_pred, grad_target)."""
+    call: one launch that forms both (the loss is symmetric in its inputs; volumes of at most 16^3
+    take the pred-gradient kernel twice, the second time with the inputs swapped). Bit for bit the
+    gradients of those two passes. Returns (loss, grad_pred, grad_target)."""
     code = _dtype_code(pf)
     _check_vols("pred", pf)
     _check_vols("target", tf, like=pf, dtype=pf.dtype)
