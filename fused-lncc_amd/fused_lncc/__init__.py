@@ -37,6 +37,19 @@ def _(pf, tf, kernel_size, smooth_dr, need_grad):
     return loss, (torch.empty_like(pf) if need_grad else pf.new_empty((0,)))
 
 
+# Both gradients from one launch (target_grad=True): the loss, the pred gradient and the target
+# gradient, each gradient in the input dtype.
+@torch.library.custom_op("fused_lncc::loss_grad_pt", mutates_args=())
+def _loss_grad_pt_op(pf: torch.Tensor, tf: torch.Tensor, kernel_size: int,
+                     smooth_dr: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return ext.loss_grad_pt(pf, tf, kernel_size, smooth_dr)
+
+
+@_loss_grad_pt_op.register_fake
+def _(pf, tf, kernel_size, smooth_dr):
+    return pf.new_empty((), dtype=torch.float32), torch.empty_like(pf), torch.empty_like(tf)
+
+
 @torch.library.custom_op("fused_lncc::scale_grad_", mutates_args=("grad",))
 def _scale_grad_op(grad: torch.Tensor, grad_out: torch.Tensor) -> None:
     ext.scale_grad_(grad, grad_out)
@@ -105,9 +118,12 @@ class _FusedLNCC(torch.autograd.Function):
             S = pred.shape[2:]
             pf = pred.reshape(N * C, *S)
             tf = target.reshape(N * C, *S)
-            loss, grad = torch.ops.fused_lncc.loss_grad(pf, tf, kernel_size, smooth_dr, need)
-            if need_t:
-                _, gt = torch.ops.fused_lncc.loss_grad(tf, pf, kernel_size, smooth_dr, True)
+            if need and need_t:
+                loss, grad, gt = torch.ops.fused_lncc.loss_grad_pt(pf, tf, kernel_size, smooth_dr)
+            else:
+                loss, grad = torch.ops.fused_lncc.loss_grad(pf, tf, kernel_size, smooth_dr, need)
+                if need_t:
+                    _, gt = torch.ops.fused_lncc.loss_grad(tf, pf, kernel_size, smooth_dr, True)
         else:
             # the library reads (N, C, D, H, W) as N*C volumes; grad comes back in pred's shape
             pf, tf = pred, target
@@ -166,6 +182,8 @@ class _FusedLNCC(torch.autograd.Function):
             gt = (sgt.float() * go).to(sgt.dtype).reshape(ctx.shape) if ctx.need_t else None
             return g, gt, None, None, None, None
         pf, tf = saved
+        if ctx.need and ctx.need_t and g is None and gt is None:
+            _, g, gt = torch.ops.fused_lncc.loss_grad_pt(pf, tf, ctx.k, ctx.dr)
         if ctx.need and g is None:
             _, g = torch.ops.fused_lncc.loss_grad(pf, tf, ctx.k, ctx.dr, True)
         if ctx.need_t and gt is None:

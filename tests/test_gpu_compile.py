@@ -81,3 +81,4 @@ def test_opcheck_custom_ops(dt):
     torch.library.opcheck(torch.ops.fused_lncc.loss_grad.default, (p, t, 5, 1e-5, True))
     torch.library.opcheck(torch.ops.fused_lncc.loss_grad.default, (p, t, 3, 1e-5, False))
     torch.library.opcheck(torch.ops.fused_lncc.forward.default, (p, t, 5, 1e-5))
+    torch.library.opcheck(torch.ops.fused_lncc.loss_grad_pt.default, (p, t, 5, 1e-5))
