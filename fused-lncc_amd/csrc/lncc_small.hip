@@ -22,7 +22,7 @@
 // range scale are those of the plane-marching kernel (lncc_fused_kernel.h). One workgroup writes
 // one float64 ncc partial sum per volume, summed over its lanes and waves in a fixed order.
 //
-// The four lanes quarters q are whole waves (256 lanes = 4 waves each), so the ranges of a
+// The four lane quarters q are whole waves (256 lanes = 4 waves each), so the ranges of a
 // quarter's line reads are wave-uniform: the first and the last quarter, whose windows reach past
 // the volume's 16 positions, run code in which those reads are compile-time zeros.
 #include "lncc_common.h"
