@@ -327,3 +327,13 @@ def test_first_use_builds_missing_library(tmp_path):
     assert out.returncode == 0, out.stderr[-3000:]
     assert "building it" in out.stderr
     assert out.stdout.strip() == f"loaded {pkg / 'fused_lncc' / 'libfused_lncc_hip.so'} True"
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with status 2 and says so, before touching a
+    device."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode == 2 and "one GPU only" in r.stderr, (r.returncode, r.stderr)
