@@ -107,3 +107,23 @@ def test_dual_kernel_against_single_passes(k, dt, dchunk, force_dchunk):
     assert loss.item() == loss1.item()
     # the same kernel on the same (swapped) inputs and the same plan: bit for bit
     assert torch.equal(gt, gt1)
+
+
+@pytest.mark.parametrize("name", ["headline", "bf16"])
+def test_dual_kernel_bitwise_at_full_size(name):
+    """At the headline workload (2,16,128^3) fp32 k=7 and its bf16 k=5 variant, the one-launch
+    kernel's two gradients equal the pred-gradient kernel's and the swapped pass's bit for bit, and
+    its loss equals the pred pass's."""
+    from fused_lncc import ext
+
+    p, t = wl.make_inputs(name)
+    k = wl.WORKLOADS[name]["k"]
+    pf, tf = p.to(DEV), t.to(DEV)
+    print(f"dual at {name} {tuple(p.shape)} {p.dtype} k={k}", flush=True)
+    loss, gp, gt = ext.loss_grad_pt(pf, tf, k, 1e-5)
+    loss1, gp1 = ext.loss_grad(pf, tf, k, 1e-5, True)
+    assert torch.equal(gp, gp1)
+    del gp1
+    gt1 = ext.grad_only(tf, pf, k, 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(gt, gt1) and loss.item() == loss1.item()
